@@ -1,0 +1,130 @@
+"""The CPU oracle against the reference's golden vectors and against closed forms.
+
+The golden files were written by the reference's own code (tests/golden/make_golden.py):
+ProductPostingIndex.build on CPU (state.py:477-948) and, under the Triton CPU
+interpreter, the flat scoring and RESIDENT selection kernels (fused_select.py).
+"""
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import reference_cpu as ref
+from synth import golden_keys, keys_checksum
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _load(name):
+    return torch.load(GOLDEN / name, weights_only=True)
+
+
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("kmeans_*.pt")))
+def test_block_build_matches_the_reference_bit_for_bit(name):
+    g = _load(name)
+    length, hkv, d = int(g["length"]), int(g["hkv"]), int(g["d"])
+    k_pre = golden_keys(length, hkv, d, int(g["seed"]), mixture=name.endswith("_mix.pt"))
+    assert torch.allclose(keys_checksum(k_pre), g["keys_checksum"], rtol=0, atol=1e-6), \
+        "the key generator changed"
+    product = ref.routing_normalize_keys(k_pre)
+    if "product" in g:
+        assert torch.equal(product, g["product"])
+    idx = ref.build_flat_index(product, codebook_seed=int(g["codebook_seed"]),
+                               min_clusters_log2=int(g["min_log2"]))
+    assert torch.equal(idx["sizes"], g["sizes"])
+    assert torch.equal(idx["indptr"], g["indptr"])
+    assert torch.equal(idx["posting"], g["posting"])
+    assert torch.equal(idx["inverse"], g["inverse"])
+    assert torch.equal(idx["codebooks"], g["codebooks"])
+
+
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("select_*.pt")))
+def test_scores_match_the_reference_kernel(name):
+    g = _load(name)
+    prob = ref.mixture_probs(g["vectors"], None, g["codebooks"], float(g["tau"]))
+    # the kernel sums bf16 products in another order; the score is a log-prob
+    assert torch.allclose(prob.clamp_min(1e-30).log(), g["prob"].clamp_min(1e-30).log(),
+                          atol=1e-3, rtol=1e-4)
+    want = ref.mixture_probs_fp64(g["vectors"], None, g["codebooks"], float(g["tau"]))
+    assert torch.allclose(prob.double(), want, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("select_*.pt")))
+def test_bisection_matches_the_reference_kernel(name):
+    g = _load(name)
+    out = ref.theta_select(g["prob"], g["sizes"], beta=float(g["beta"]),
+                           target_tokens=float(g["target"]), g_union=int(g["g_union"]))
+    assert torch.equal(out["qmask"], g["qmask"])
+    assert torch.equal(out["bitmask"], g["bitmask"])
+    assert torch.equal(out["counts"], g["counts"])
+    assert torch.equal(out["tokens"], g["tokens"])
+
+
+def test_sorted_rule_is_a_subset_of_the_bisection():
+    g = _load("select_q64_c128.pt")
+    out = ref.theta_select(g["prob"], g["sizes"], beta=0.25, target_tokens=512, g_union=32)
+    sorted_sel = ref.sorted_select(out["score"], g["sizes"], 512, g_union=32)
+    assert not (sorted_sel & ~out["sel"]).any()
+    # the extra clusters sit within range * 2^-16 of the sorted cut
+    extra = out["sel"] & ~sorted_sel
+    rng = (out["score"].max(-1).values - torch.where(out["score"] > -1e38, out["score"],
+           torch.full_like(out["score"], 1e38)).min(-1).values)
+    for q, h, c in torch.nonzero(extra).tolist():
+        assert out["score"][q, h, c] >= out["theta"][q, h]
+        assert out["score"][q, h, c] - out["theta"][q, h] <= rng[q, h] * 2 ** -15 + 2e-5
+
+
+def test_dead_clusters_are_never_selected_and_all_fit_takes_everything():
+    gen = torch.Generator().manual_seed(5)
+    prob = torch.rand(8, 2, 64, generator=gen)
+    sizes = torch.randint(0, 30, (1, 2, 64), generator=gen, dtype=torch.int32)
+    sizes[..., ::3] = 0
+    out = ref.theta_select(prob, sizes, beta=0.25, target_tokens=10 ** 6, g_union=8)
+    live = sizes[0] > 0
+    assert torch.equal(out["sel"], live[None].expand_as(out["sel"]))
+    out = ref.theta_select(prob, sizes, beta=0.25, target_tokens=100, g_union=8)
+    assert not (out["sel"] & ~live[None]).any()
+    have = (out["sel"] * sizes[0][None]).sum(-1)
+    assert (have >= 100).all()
+
+
+def test_router_closed_form():
+    x = torch.randn(7, 4, 256).to(torch.bfloat16)
+    v = ref.trivial_router_vectors(x, 1)
+    n = v.float().norm(dim=-1)
+    assert torch.allclose(n, torch.ones_like(n), atol=4e-3)
+    # idempotent up to one bf16 rounding
+    assert torch.allclose(ref.trivial_router_vectors(v, 1).float(), v.float(), atol=2 ** -8)
+
+
+def test_cluster_count_rule():
+    assert ref.num_flat_clusters(131072) == 128
+    assert ref.num_flat_clusters(524288) == 256
+    assert ref.num_flat_clusters(32768) == 128
+    assert ref.num_flat_clusters(8192) == 128
+    assert ref.num_flat_clusters(512) == 128
+    assert ref.num_flat_clusters(100) == 64
+
+
+def test_lse_merge_closed_form():
+    o = torch.randn(3, 5)
+    out, lse = ref.lse_merge(o, torch.zeros(3), o, torch.zeros(3))
+    assert torch.allclose(out, o.double())
+    assert torch.allclose(lse, torch.full((3,), math.log(2.0), dtype=torch.float64))
+
+
+def test_reverse_index_is_the_transpose():
+    gen = torch.Generator().manual_seed(1)
+    sel = torch.rand(50, 2, 64, generator=gen) < 0.2
+    live = torch.rand(2, 64, generator=gen) < 0.9
+    counts, indptr, qvals = ref.reverse_index(sel, live)
+    for h in range(2):
+        for c in range(64):
+            e0 = int(indptr[h * 64 + c])
+            n = int(counts[h, c])
+            got = qvals[e0:e0 + n].tolist()
+            want = torch.nonzero(sel[:, h, c] & live[h, c]).flatten().tolist()
+            assert got == want
