@@ -1,0 +1,443 @@
+// S5 KV-outer sparse prefill attention and S6 log-sum-exp combine for gfx950.
+//
+// Reference behaviour (pfnet-research/semantic-block-sparse-attention):
+//   kv_outer.py:482-816        kv_outer_attention: one FA3 varlen call per
+//                              (cluster, KV head) over its visible rows, whose
+//                              query rows are the queries that selected it
+//                              (Q heads folded into rows), plus an exactly
+//                              causal FA3 call over the chunk's own window
+//   fused_prefill.py:155-189   dense causal attention for the early chunks
+//   kv_outer.py:370-428        _combine_grouped_kernel (query-major LSE fold)
+//
+// Design (MI355X): one persistent kernel walks a work list of items.  An item
+// is (KV head, cluster or the local window, a tile of 128/G queries); its
+// 128 (query, head) rows run against the cluster's contiguous packed run (or
+// the prompt-order window, causally masked) in 64-key tiles.  Both GEMMs are
+// on bf16 MFMA 16x16x32 in the transposed form S^T = K Q^T, O^T = V^T P^T,
+// so the softmax probabilities come out of the first MFMA already in the
+// B-operand layout of the second and never pass through LDS.
+#include "sbsa_common.h"
+
+namespace {
+
+struct AttnArgs {
+  const bf16_t* q;          // [Qc, Hq, D] chunk queries
+  int64_t q_sq, q_sh;
+  const bf16_t* packed;     // [2, Lp, Hkv, D] cluster-ordered K/V
+  int64_t packed_len;
+  const bf16_t* korig;      // prompt-order keys from position wstart: k[pos - wstart, h, :]
+  const bf16_t* vorig;      // prompt-order values, same rows
+  int64_t o_st, o_sh;       // their token / head strides (elements)
+  const int32_t* indptr;    // [Hkv, C+1] packed run starts
+  const int32_t* nvis;      // [Hkv, C] visible rows per cluster
+  const int32_t* rev_indptr;// [Hkv*C + 1]
+  const int32_t* qvals;     // [nnz] query slots per (head, cluster)
+  const int4* items;
+  const int32_t* n_items;
+  int32_t* counter;
+  bf16_t* part_o;           // [nnz, G, D]
+  float* part_lse;          // [nnz, G]
+  bf16_t* local_o;          // [Qc, Hq, D] strided
+  int64_t lo_sq, lo_sh;
+  float* local_lse;         // [Qc, Hq] or null
+  int Hkv, C, Hq;
+  int64_t chunk_start, wstart;
+  float scale_log2;         // sm_scale * log2(e)
+};
+
+constexpr int KT = 64;      // keys per tile
+
+template <int D, int G>
+__global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
+  constexpr int KS = D / 32;
+  constexpr int DB = D / 16;
+  constexpr int LDK = D + 8;
+  constexpr int LDV = KT + 4;
+  constexpr int DPT = D / 16;            // V dims per thread in the transposing load
+  __shared__ __attribute__((aligned(16))) bf16_t sK[KT * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t sV[D * LDV];
+  __shared__ int s_item;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int total = *a.n_items;
+  const float NEG_INF = -INFINITY;
+
+  while (true) {
+    if (threadIdx.x == 0) s_item = atomicAdd(a.counter, 1);
+    __syncthreads();
+    const int idx = s_item;
+    __syncthreads();
+    if (idx >= total) break;
+    const int4 it = a.items[idx];
+    const int h = it.x, c = it.y, qb = it.z, qn = it.w;
+    const bool local = c < 0;
+    const bf16_t* kp;
+    const bf16_t* vp;
+    int64_t rs;
+    int nkeys;
+    int64_t entry0 = 0;
+    if (local) {
+      kp = a.korig + (int64_t)h * a.o_sh;   // row 0 is position wstart
+      vp = a.vorig + (int64_t)h * a.o_sh;
+      rs = a.o_st;
+      nkeys = (int)(a.chunk_start + qb + qn - a.wstart);
+    } else {
+      int64_t r0 = a.indptr[h * (a.C + 1) + c];
+      kp = a.packed + r0 * a.Hkv * D + (int64_t)h * D;
+      vp = kp + a.packed_len * a.Hkv * D;
+      rs = (int64_t)a.Hkv * D;
+      nkeys = a.nvis[h * a.C + c];
+      entry0 = (int64_t)a.rev_indptr[h * a.C + c] + qb;
+    }
+
+    // Q rows of this wave: R = wave*32 + rb*16 + l16 -> (slot i, head j)
+    u32x4_t qr[2][KS];
+    int qlim[2];
+    int qidx_r[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int R = wave * 32 + rb * 16 + l16;
+      const int i = R / G, j = R % G;
+      const bool ok = i < qn;
+      int qidx = 0;
+      if (ok) qidx = local ? qb + i : a.qvals[entry0 + i];
+      qidx_r[rb] = qidx;
+      qlim[rb] = local ? (int)(a.chunk_start + qidx - a.wstart) : 0x7fffffff;
+      const bf16_t* src = a.q + (int64_t)qidx * a.q_sq + (int64_t)(h * G + j) * a.q_sh + lg * 8;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        qr[rb][s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
+    }
+
+    f32x4_t o[DB][2];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      o[db][0] = f32x4_t{0, 0, 0, 0};
+      o[db][1] = f32x4_t{0, 0, 0, 0};
+    }
+    float m_run[2] = {NEG_INF, NEG_INF};
+    float l_run[2] = {0.f, 0.f};
+
+    for (int t0 = 0; t0 < nkeys; t0 += KT) {
+      // K tile: row-major, padded rows
+#pragma unroll
+      for (int k = 0; k < (KT * D / 8) / 256; ++k) {
+        const int e = threadIdx.x + 256 * k;
+        const int r = e / (D / 8), ch = e % (D / 8);
+        u32x4_t v = u32x4_t{0, 0, 0, 0};
+        if (t0 + r < nkeys) v = *reinterpret_cast<const u32x4_t*>(kp + (int64_t)(t0 + r) * rs + ch * 8);
+        *reinterpret_cast<u32x4_t*>(&sK[r * LDK + ch * 8]) = v;
+      }
+      // V tile transposed: thread -> keys 4kq..4kq+3, dims dc*DPT..+DPT
+      {
+        const int kq = threadIdx.x & 15, dc = threadIdx.x >> 4;
+        bf16_t vv[4][DPT];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int key = t0 + kq * 4 + kk;
+          const bool ok = key < nkeys;
+          const bf16_t* src = vp + (int64_t)key * rs + dc * DPT;
+          if constexpr (DPT % 8 == 0) {
+#pragma unroll
+            for (int u = 0; u < DPT / 8; ++u) {
+              u32x4_t w = ok ? *reinterpret_cast<const u32x4_t*>(src + u * 8) : u32x4_t{0, 0, 0, 0};
+              __builtin_memcpy(&vv[kk][u * 8], &w, 16);
+            }
+          } else {
+            u32x2_t w = ok ? *reinterpret_cast<const u32x2_t*>(src) : u32x2_t{0, 0};
+            __builtin_memcpy(&vv[kk][0], &w, 8);
+          }
+        }
+#pragma unroll
+        for (int dd = 0; dd < DPT; ++dd) {
+          u32x2_t w;
+          w.x = (uint32_t)vv[0][dd] | ((uint32_t)vv[1][dd] << 16);
+          w.y = (uint32_t)vv[2][dd] | ((uint32_t)vv[3][dd] << 16);
+          *reinterpret_cast<u32x2_t*>(&sV[(dc * DPT + dd) * LDV + kq * 4]) = w;
+        }
+      }
+      __syncthreads();
+
+      // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of row (rb, l16)
+      f32x4_t sacc[4][2];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sacc[kb][0] = f32x4_t{0, 0, 0, 0};
+        sacc[kb][1] = f32x4_t{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          u32x4_t ka = *reinterpret_cast<const u32x4_t*>(&sK[(kb * 16 + l16) * LDK + s * 32 + lg * 8]);
+          sacc[kb][0] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[0][s]), sacc[kb][0]);
+          sacc[kb][1] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[1][s]), sacc[kb][1]);
+        }
+      }
+
+      // online softmax in the log2 domain
+      u32x4_t pb[2][2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        float mx = NEG_INF;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = t0 + kb * 16 + lg * 4 + i;
+            float v = sacc[kb][rb][i] * a.scale_log2;
+            v = (key < nkeys && key <= qlim[rb]) ? v : NEG_INF;
+            sacc[kb][rb][i] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[rb], mx);
+        const float m_use = (m_new == NEG_INF) ? 0.f : m_new;
+        const float alpha = exp2f(m_run[rb] - m_use);
+        float sum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float p = exp2f(sacc[kb][rb][i] - m_use);
+            sacc[kb][rb][i] = p;
+            sum += p;
+          }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        l_run[rb] = l_run[rb] * alpha + sum;
+        m_run[rb] = m_new;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db][rb] *= alpha;
+        // B operand of P^T for key pairs (2t2, 2t2+1)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
+          pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
+          pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
+          pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
+        }
+      }
+
+      // O^T += V^T P^T
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const bf16_t* vrow = &sV[(db * 16 + l16) * LDV + t2 * 32 + lg * 4];
+          u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
+          u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
+          u32x4_t va = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+          o[db][0] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[0][t2]), o[db][0]);
+          o[db][1] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[1][t2]), o[db][1]);
+        }
+      }
+      __syncthreads();
+    }
+
+    // epilogue: normalise, write the partial (or the local window) and its LSE
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int R = wave * 32 + rb * 16 + l16;
+      const int i = R / G, j = R % G;
+      if (i >= qn) continue;
+      const float l = l_run[rb];
+      const float inv = (l > 0.f) ? 1.0f / l : 0.f;
+      const float lse = (l > 0.f) ? (m_run[rb] + log2f(l)) * 0.69314718055994531f : NEG_INF;
+      bf16_t* dst;
+      float* ldst;
+      if (local) {
+        dst = a.local_o + (int64_t)qidx_r[rb] * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh;
+        ldst = a.local_lse ? a.local_lse + (int64_t)qidx_r[rb] * a.Hq + h * G + j : nullptr;
+      } else {
+        dst = a.part_o + ((entry0 + i) * G + j) * D;
+        ldst = a.part_lse + (entry0 + i) * G + j;
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        u32x2_t w;
+        w.x = pack2bf(o[db][rb][0] * inv, o[db][rb][1] * inv);
+        w.y = pack2bf(o[db][rb][2] * inv, o[db][rb][3] * inv);
+        *reinterpret_cast<u32x2_t*>(dst + db * 16 + lg * 4) = w;
+      }
+      if (lg == 0 && ldst) *ldst = lse;
+    }
+  }
+}
+
+// S6: per (query, KV head), one wave.  Seeds with the local window, then
+// folds the query's cluster partials in cluster order (query-major order of
+// the reference's entries).  Each lane owns E = G*D/64 consecutive values of
+// one head.
+template <int D, int G>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const int32_t* __restrict__ qmask, const int32_t* __restrict__ nvis,
+    const int32_t* __restrict__ rev_indptr, const int32_t* __restrict__ qrank,
+    const bf16_t* __restrict__ part_o, const float* __restrict__ part_lse,
+    const bf16_t* __restrict__ local_o, int64_t lo_sq, int64_t lo_sh,
+    const float* __restrict__ local_lse, bf16_t* __restrict__ out, int64_t out_sq, int64_t out_sh,
+    float* __restrict__ out_lse, int Qc, int Hkv, int C) {
+  constexpr int E = G * D / 64;
+  static_assert(E >= 1 && D % E == 0, "lane share");
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= (int64_t)Qc * Hkv) return;
+  const int qi = (int)(gw / Hkv), h = (int)(gw % Hkv);
+  const int j = (lane * E) / D, d0 = (lane * E) % D;
+  const int Hq = Hkv * G;
+  float acc[E];
+  float m = local_lse[(int64_t)qi * Hq + h * G + j];
+  {
+    const bf16_t* src = local_o + (int64_t)qi * lo_sq + (int64_t)(h * G + j) * lo_sh + d0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = bf2f(src[e]);
+  }
+  float den = 1.f;
+  const int W = C / 32;
+  const int32_t* qm = qmask + ((int64_t)qi * Hkv + h) * W;
+  const int32_t* qr = qrank + ((int64_t)qi * Hkv + h) * C;
+  for (int w = 0; w < W; ++w) {
+    uint32_t bits = (uint32_t)qm[w];
+    while (bits) {
+      const int b = __builtin_ctz(bits);
+      bits &= bits - 1;
+      const int c = w * 32 + b;
+      if (nvis[h * C + c] <= 0) continue;
+      const int64_t entry = (int64_t)rev_indptr[h * C + c] + qr[c];
+      const float le = part_lse[entry * G + j];
+      const float nm = fmaxf(m, le);
+      const float sc = expf(m - nm);
+      const float wt = expf(le - nm);
+      const bf16_t* src = part_o + (entry * G + j) * D + d0;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = acc[e] * sc + bf2f(src[e]) * wt;
+      den = den * sc + wt;
+      m = nm;
+    }
+  }
+  const float inv = 1.0f / fmaxf(den, 1e-30f);
+  bf16_t* dst = out + (int64_t)qi * out_sq + (int64_t)(h * G + j) * out_sh + d0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) dst[e] = f2bf(acc[e] * inv);
+  if (out_lse && (lane * E) % D == 0) out_lse[(int64_t)qi * Hq + h * G + j] = m + logf(den);
+}
+
+template <int D, int G>
+int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), 0, stream, a);
+  return SBSA_OK;
+}
+
+template <int D, int G>
+int launch_combine(const int32_t* qmask, const int32_t* nvis, const int32_t* rev_indptr,
+                   const int32_t* qrank, const bf16_t* part_o, const float* part_lse,
+                   const bf16_t* local_o, int64_t lo_sq, int64_t lo_sh, const float* local_lse,
+                   bf16_t* out, int64_t out_sq, int64_t out_sh, float* out_lse, int Qc, int Hkv,
+                   int C, hipStream_t stream) {
+  int64_t waves = (int64_t)Qc * Hkv;
+  hipLaunchKernelGGL((combine_kernel<D, G>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                     stream, qmask, nvis, rev_indptr, qrank, part_o, part_lse, local_o, lo_sq,
+                     lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C);
+  return SBSA_OK;
+}
+
+#define SBSA_DISPATCH_DG(D_, G_, FN, ...)                            \
+  do {                                                               \
+    if (D_ == 128 && G_ == 1) return FN<128, 1>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 2) return FN<128, 2>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 4) return FN<128, 4>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 8) return FN<128, 8>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 1) return FN<256, 1>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 2) return FN<256, 2>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 4) return FN<256, 4>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 8) return FN<256, 8>(__VA_ARGS__);        \
+    return SBSA_ERR_UNSUPPORTED;                                     \
+  } while (0)
+
+int attn_dispatch(int D, int G, const AttnArgs& a, int grid, hipStream_t stream) {
+  SBSA_DISPATCH_DG(D, G, launch_attn, a, grid, stream);
+}
+
+int combine_dispatch(int D, int G, const int32_t* qmask, const int32_t* nvis,
+                     const int32_t* rev_indptr, const int32_t* qrank, const bf16_t* part_o,
+                     const float* part_lse, const bf16_t* local_o, int64_t lo_sq, int64_t lo_sh,
+                     const float* local_lse, bf16_t* out, int64_t out_sq, int64_t out_sh,
+                     float* out_lse, int Qc, int Hkv, int C, hipStream_t stream) {
+  SBSA_DISPATCH_DG(D, G, launch_combine, qmask, nvis, rev_indptr, qrank, part_o, part_lse, local_o,
+                   lo_sq, lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queries,
+                        int num_q_heads, int num_kv_heads, int dim, const void* packed,
+                        int64_t packed_len, const void* k_orig, const void* v_orig, int64_t o_st,
+                        int64_t o_sh, const int32_t* indptr, const int32_t* nvis, int num_clusters,
+                        const int32_t* rev_indptr, const int32_t* qvals, const void* items,
+                        const int32_t* n_items, int32_t* counter, void* part_o, float* part_lse,
+                        void* local_o, int64_t lo_sq, int64_t lo_sh, float* local_lse,
+                        int64_t chunk_start, int64_t wstart, float sm_scale, int grid,
+                        hipStream_t stream) {
+  if (!q || !k_orig || !v_orig || !items || !n_items || !counter || !local_o) return SBSA_ERR_ARG;
+  if (num_kv_heads < 1 || num_q_heads % num_kv_heads) return SBSA_ERR_ARG;
+  if (q_sq % 8 || q_sh % 8 || o_st % 8 || o_sh % 8 || lo_sq % 4 || lo_sh % 4) return SBSA_ERR_ARG;
+  if (chunk_start < wstart || wstart < 0) return SBSA_ERR_ARG;
+  AttnArgs a;
+  a.q = (const bf16_t*)q;
+  a.q_sq = q_sq;
+  a.q_sh = q_sh;
+  a.packed = (const bf16_t*)packed;
+  a.packed_len = packed_len;
+  a.korig = (const bf16_t*)k_orig;
+  a.vorig = (const bf16_t*)v_orig;
+  a.o_st = o_st;
+  a.o_sh = o_sh;
+  a.indptr = indptr;
+  a.nvis = nvis;
+  a.rev_indptr = rev_indptr;
+  a.qvals = qvals;
+  a.items = (const int4*)items;
+  a.n_items = n_items;
+  a.counter = counter;
+  a.part_o = (bf16_t*)part_o;
+  a.part_lse = part_lse;
+  a.local_o = (bf16_t*)local_o;
+  a.lo_sq = lo_sq;
+  a.lo_sh = lo_sh;
+  a.local_lse = local_lse;
+  a.Hkv = num_kv_heads;
+  a.C = num_clusters;
+  a.Hq = num_q_heads;
+  a.chunk_start = chunk_start;
+  a.wstart = wstart;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  if (grid < 1) grid = 512;
+  int rc = attn_dispatch(dim, num_q_heads / num_kv_heads, a, grid, stream);
+  if (rc) return rc;
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_t* rev_indptr,
+                         const int32_t* qrank, const void* part_o, const float* part_lse,
+                         const void* local_o, int64_t lo_sq, int64_t lo_sh, const float* local_lse,
+                         void* out, int64_t out_sq, int64_t out_sh, float* out_lse,
+                         int num_queries, int num_q_heads, int num_kv_heads, int dim,
+                         int num_clusters, hipStream_t stream) {
+  if (!qmask || !nvis || !rev_indptr || !qrank || !local_o || !local_lse || !out) return SBSA_ERR_ARG;
+  if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_clusters % 32) return SBSA_ERR_ARG;
+  if (num_queries == 0) return SBSA_OK;
+  int rc = combine_dispatch(dim, num_q_heads / num_kv_heads, qmask, nvis, rev_indptr, qrank,
+                            (const bf16_t*)part_o, part_lse, (const bf16_t*)local_o, lo_sq, lo_sh,
+                            local_lse, (bf16_t*)out, out_sq, out_sh, out_lse, num_queries,
+                            num_kv_heads, num_clusters, stream);
+  if (rc) return rc;
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,446 @@
+// S2 centroid scoring + S3 budget selection, S3c causal snapshot, and S4 the
+// reverse index with the work list of the KV-outer prefill, for gfx950.
+//
+// Reference behaviour (pfnet-research/semantic-block-sparse-attention):
+//   fused_select.py:1062-1247  _flat_scores_qtiled_kernel (score, LSE, mixture prob)
+//   fused_select.py:604-646    _streaming_select_kernel RESIDENT (bisection, bitmask, qmask)
+//   fused_select.py:806-919    theta_select_bitmask_flat (the contract)
+//   fused_prefill.py:126-135   CausalSnapshot.advance
+//   kv_outer.py:41-173, 254-329 build_reverse_index
+#include "sbsa_common.h"
+
+namespace {
+
+// ------------------------------------------------------------- S2 + S3 -----
+// One block = QT queries x one KV head.  Rows of the score GEMM are
+// (query, component) pairs, R = QT * G of them; the four waves split the
+// clusters.  Scores live in LDS; each wave then selects for its queries.
+struct SelectArgs {
+  const bf16_t* vectors;   // [Q, Hq, D] routing vectors
+  int64_t v_sq, v_sh;      // element strides
+  const float* logmix;     // [Q, Hq] or null (uniform: 0)
+  const bf16_t* codebooks; // [Hkv, 2, C, D/2]
+  const int32_t* sizes;    // sizes[b * s_nb + h * s_h + c]
+  int64_t s_nb, s_h;
+  int32_t* bitmask;        // [NB, Hkv, C/32] (atomic OR) or null
+  int32_t* qmask;          // [Q, Hkv, C/32] or null
+  int32_t* counts;         // [Q, Hkv] or null
+  int32_t* tokens;         // [Q, Hkv] or null
+  float* prob_out;         // [Q, Hkv, C] or null
+  float* theta_out;        // [Q, Hkv] or null
+  int Q, Hq, Hkv, C, G, g_union, iters, sink;
+  float inv_temp, beta, target;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) {
+  constexpr int KS = D / 32;
+  constexpr int LDQ = D + 8;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  bf16_t* sq = reinterpret_cast<bf16_t*>(smem);                      // [R][LDQ]
+  float* ssc = reinterpret_cast<float*>(smem + (size_t)R * LDQ * 2);  // [R][C+1]
+  const int C = a.C, G = a.G;
+  const int LDS_C = C + 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = blockIdx.y;
+  const int QT = R / G;
+  const int q0 = blockIdx.x * QT;
+  const int half = D / 2;
+
+  // Q tile -> LDS (rows r = query*G + component)
+  for (int e = threadIdx.x; e < R * (D / 8); e += 256) {
+    int r = e / (D / 8), ch = e % (D / 8);
+    int q = q0 + r / G, t = r % G;
+    u32x4_t v = u32x4_t{0, 0, 0, 0};
+    if (q < a.Q)
+      v = *reinterpret_cast<const u32x4_t*>(a.vectors + (int64_t)q * a.v_sq + (int64_t)(h * G + t) * a.v_sh + ch * 8);
+    *reinterpret_cast<u32x4_t*>(&sq[r * LDQ + ch * 8]) = v;
+  }
+  __syncthreads();
+
+  // scores: each wave takes C/4 clusters (a multiple of 16)
+  const int cols_per_wave = C / 4;
+  const bf16_t* cb = a.codebooks + (int64_t)h * 2 * C * half;
+  for (int cbk = 0; cbk < cols_per_wave / 16; ++cbk) {
+    const int col0 = wave * cols_per_wave + cbk * 16;
+    const int cc = col0 + (lane & 15);
+    u32x4_t bop[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      int d = s * 32 + (lane >> 4) * 8;
+      int part = d / half;
+      bop[s] = *reinterpret_cast<const u32x4_t*>(cb + ((int64_t)part * C + cc) * half + (d - part * half));
+    }
+    for (int rb = 0; rb < R / 16; ++rb) {
+      f32x4_t acc = f32x4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        u32x4_t aop = *reinterpret_cast<const u32x4_t*>(&sq[(rb * 16 + (lane & 15)) * LDQ + s * 32 + (lane >> 4) * 8]);
+        acc = mfma16x16x32(as_bf16x8(aop), as_bf16x8(bop[s]), acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ssc[(rb * 16 + (lane >> 4) * 4 + i) * LDS_C + cc] = acc[i] * a.inv_temp;
+    }
+  }
+  __syncthreads();
+
+  // per row: lse over C, then w = exp(s - lse + logmix) in place
+  for (int r = wave; r < R; r += 4) {
+    float* row = ssc + r * LDS_C;
+    float m = -INFINITY;
+    for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int c = lane; c < C; c += 64) l += expf(row[c] - m);
+    l = wave_sum(l);
+    float lse = m + logf(l);
+    int q = q0 + r / G, t = r % G;
+    float lm = 0.f;
+    if (a.logmix && q < a.Q) lm = a.logmix[(int64_t)q * a.Hq + h * G + t];
+    for (int c = lane; c < C; c += 64) row[c] = expf(row[c] - lse + lm);
+  }
+  __syncthreads();
+
+  // selection, one wave per query; lane holds clusters lane + 64k
+  const int W = C / 32;
+  const float NEG = -3.4e38f, POS = 3.4e38f;
+  for (int qi = wave; qi < QT; qi += 4) {
+    const int q = q0 + qi;
+    if (q >= a.Q) break;
+    const int b = q / a.g_union;
+    const int32_t* sz = a.sizes + (int64_t)b * a.s_nb + (int64_t)h * a.s_h;
+    float score[16], size[16];
+    float real_size[16];
+    const int nk = C / 64;
+    float hi = -INFINITY, lo = INFINITY;
+    long long live_total = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      score[k] = NEG;
+      size[k] = 0.f;
+      real_size[k] = 0.f;
+      if (k < nk) {
+        int c = lane + 64 * k;
+        float p = 0.f;
+        for (int t = 0; t < G; ++t) p += ssc[(qi * G + t) * LDS_C + c];
+        if (a.prob_out) a.prob_out[((int64_t)q * a.Hkv + h) * C + c] = p;
+        float rs = (float)sz[c];
+        float s = (a.sink > 0 && c == 0) ? 0.f : rs;  // the sink is hidden from the search
+        real_size[k] = rs;
+        size[k] = s;
+        bool live = s > 0.f;
+        float sc = logf(fmaxf(p, 1e-38f));
+        if (a.beta != 0.f) sc = sc - a.beta * logf(1.0f + s);
+        sc = live ? sc : NEG;
+        score[k] = sc;
+        hi = fmaxf(hi, sc);
+        lo = fminf(lo, live ? sc : POS);
+        if (live) live_total += (long long)s;
+      }
+    }
+    hi = wave_max(hi) + 1e-6f;
+    lo = wave_min(lo) - 1e-6f;
+    lo = fminf(lo, hi - 1e-5f);
+    live_total = wave_sum_i64(live_total);
+    float budget = a.target;
+    if (a.sink > 0) budget = fmaxf(a.target - (float)a.sink, 0.f);
+    const bool all_fit = (float)live_total < budget;
+    for (int it = 0; it < a.iters; ++it) {
+      float mid = (lo + hi) * 0.5f;
+      long long above = 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (k < nk && score[k] >= mid) above += (long long)size[k];
+      above = wave_sum_i64(above);
+      bool reach = (float)above >= budget;
+      lo = reach ? mid : lo;
+      hi = reach ? hi : mid;
+    }
+    const float theta = all_fit ? NEG : lo;
+    int nsel = 0;
+    long long ntok = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k < nk) {
+        int c = lane + 64 * k;
+        bool sel = (size[k] > 0.f && score[k] >= theta) || (a.sink > 0 && c == 0 && real_size[k] > 0.f);
+        nsel += sel ? 1 : 0;
+        ntok += sel ? (long long)real_size[k] : 0;
+        uint64_t ball = __ballot(sel);
+        if (lane < 2) {
+          uint32_t word = (uint32_t)(ball >> (32 * lane));
+          int wi = 2 * k + lane;
+          if (a.qmask) a.qmask[((int64_t)q * a.Hkv + h) * W + wi] = (int32_t)word;
+          if (a.bitmask && word) atomicOr((unsigned int*)&a.bitmask[((int64_t)b * a.Hkv + h) * W + wi], word);
+        }
+      }
+    }
+    nsel = wave_sum_i32(nsel);
+    ntok = wave_sum_i64(ntok);
+    if (lane == 0) {
+      if (a.counts) a.counts[(int64_t)q * a.Hkv + h] = nsel;
+      if (a.tokens) a.tokens[(int64_t)q * a.Hkv + h] = (int32_t)ntok;
+      if (a.theta_out) a.theta_out[(int64_t)q * a.Hkv + h] = theta;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- S3c ------
+// |{keys of cluster c with position < limit}|: the run is position-sorted.
+__global__ void causal_sizes_kernel(const int32_t* __restrict__ posting, int64_t width,
+                                    const int32_t* __restrict__ indptr,
+                                    const int32_t* __restrict__ sizes, int hkv, int C,
+                                    int64_t limit, int32_t* __restrict__ out) {
+  int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= hkv * C) return;
+  int h = e / C, c = e % C;
+  const int32_t* run = posting + (int64_t)h * width + indptr[h * (C + 1) + c];
+  int lo = 0, hi = sizes[e];
+  while (lo < hi) {
+    int mid = (lo + hi) >> 1;
+    if ((int64_t)run[mid] < limit) lo = mid + 1;
+    else hi = mid;
+  }
+  out[e] = lo;
+}
+
+// ----------------------------------------------------------------- S4 ------
+// Per (head, cluster): the queries whose qmask has the cluster (and the
+// cluster has visible rows), in query order.  Pass 0 counts, pass 1 fills
+// qvals[rev_indptr + rank] and qrank[q, h, c] = rank.
+__global__ __launch_bounds__(256) void rev_pass_kernel(int pass, const int32_t* __restrict__ qmask,
+                                                       int Q, int hkv, int C,
+                                                       const int32_t* __restrict__ nvis,
+                                                       int32_t* __restrict__ rev_counts,
+                                                       const int32_t* __restrict__ rev_indptr,
+                                                       int32_t* __restrict__ qvals,
+                                                       int32_t* __restrict__ qrank) {
+  __shared__ int wcnt[4];
+  const int hc = blockIdx.x;
+  const int h = hc / C, c = hc % C;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int W = C / 32;
+  const bool live = nvis[hc] > 0;
+  int run = 0;
+  const int base_out = (pass == 1) ? rev_indptr[hc] : 0;
+  for (int q0 = 0; q0 < Q; q0 += 256) {
+    int q = q0 + threadIdx.x;
+    bool bit = false;
+    if (live && q < Q) bit = (qmask[((int64_t)q * hkv + h) * W + (c >> 5)] >> (c & 31)) & 1;
+    uint64_t ball = __ballot(bit);
+    if (lane == 0) wcnt[wave] = __popcll(ball);
+    __syncthreads();
+    int off = run;
+    for (int w = 0; w < wave; ++w) off += wcnt[w];
+    int before = __popcll(ball & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+    if (pass == 1 && bit) {
+      int rank = off + before;
+      qvals[base_out + rank] = q;
+      qrank[((int64_t)q * hkv + h) * C + c] = rank;
+    }
+    run += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+    __syncthreads();
+  }
+  if (pass == 0 && threadIdx.x == 0) rev_counts[hc] = run;
+}
+
+// Exclusive scan of the Hkv*C counts (one block), total into rev_indptr[n].
+__global__ __launch_bounds__(1024) void rev_scan_kernel(const int32_t* __restrict__ counts, int n,
+                                                        int32_t* __restrict__ indptr,
+                                                        int64_t* __restrict__ nnz) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int base = 0; base < n; base += 1024) {
+    int i = base + threadIdx.x;
+    int v = (i < n) ? counts[i] : 0;
+    int incl = wave_incl_scan(v);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int off = carry;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    if (i < n) indptr[i] = off + incl - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = off + incl;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    indptr[n] = carry;
+    *nnz = carry;
+  }
+}
+
+// Work list of the KV-outer body: local-window items first (the longest, the
+// last query tiles, first), then one item per (head, cluster, query tile).
+// Item = {head, cluster or -1, first query slot, query count}.
+__global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __restrict__ rev_counts,
+                                                           int hkv, int C, int Qc, int QT,
+                                                           int has_local, int4* __restrict__ items,
+                                                           int32_t* __restrict__ n_items,
+                                                           int32_t* __restrict__ counter,
+                                                           int64_t cap) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int nloc = has_local ? (Qc + QT - 1) / QT : 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < nloc * hkv; e += 1024) {
+    int k = e / hkv, h = e % hkv;
+    int tile = nloc - 1 - k;
+    int qb = tile * QT;
+    int qn = min(QT, Qc - qb);
+    if (e < cap) items[e] = make_int4(h, -1, qb, qn);
+  }
+  if (threadIdx.x == 0) carry = nloc * hkv;
+  __syncthreads();
+  const int n = hkv * C;
+  for (int base = 0; base < n; base += 1024) {
+    int i = base + threadIdx.x;
+    int cnt = (i < n) ? rev_counts[i] : 0;
+    int k = (cnt + QT - 1) / QT;
+    int incl = wave_incl_scan(k);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int off = carry;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    int first = off + incl - k;
+    for (int j = 0; j < k; ++j) {
+      int qb = j * QT;
+      if (first + j < cap) items[first + j] = make_int4(i / C, i % C, qb, min(QT, cnt - qb));
+    }
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = off + incl;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *n_items = (int32_t)min((int64_t)carry, cap);
+    *counter = 0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int sbsa_score_select(const void* vectors, int64_t v_sq, int64_t v_sh, const float* logmix,
+                      const void* codebooks, const int32_t* sizes, int64_t s_nb, int64_t s_h,
+                      int num_queries, int num_q_heads, int num_kv_heads, int num_clusters,
+                      int dim, int g_union, float inv_temperature, float beta,
+                      float target_tokens, int iters, int sink_tokens, int32_t* bitmask,
+                      int32_t* qmask, int32_t* counts, int32_t* tokens, float* prob_out,
+                      float* theta_out, hipStream_t stream) {
+  if (!vectors || !codebooks || !sizes || num_queries < 0 || num_kv_heads < 1) return SBSA_ERR_ARG;
+  if (num_q_heads % num_kv_heads || g_union < 1 || iters < 0) return SBSA_ERR_ARG;
+  if (v_sh % 8 || v_sq % 8) return SBSA_ERR_ARG;
+  const int G = num_q_heads / num_kv_heads;
+  const int C = num_clusters;
+  if (C % 64 || C > 1024 || C < 64) return SBSA_ERR_UNSUPPORTED;
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return SBSA_ERR_UNSUPPORTED;
+  if (num_queries == 0) return SBSA_OK;
+  int R = (C <= 256) ? 64 : (C <= 512 ? 32 : 16);
+  if (R < G) R = G;
+  if (R % 16) R = 16;
+  SelectArgs a;
+  a.vectors = (const bf16_t*)vectors;
+  a.v_sq = v_sq;
+  a.v_sh = v_sh;
+  a.logmix = logmix;
+  a.codebooks = (const bf16_t*)codebooks;
+  a.sizes = sizes;
+  a.s_nb = s_nb;
+  a.s_h = s_h;
+  a.bitmask = bitmask;
+  a.qmask = qmask;
+  a.counts = counts;
+  a.tokens = tokens;
+  a.prob_out = prob_out;
+  a.theta_out = theta_out;
+  a.Q = num_queries;
+  a.Hq = num_q_heads;
+  a.Hkv = num_kv_heads;
+  a.C = C;
+  a.G = G;
+  a.g_union = g_union;
+  a.iters = iters;
+  a.sink = sink_tokens;
+  a.inv_temp = inv_temperature;
+  a.beta = beta;
+  a.target = target_tokens;
+  const int QT = R / G;
+  dim3 grid((num_queries + QT - 1) / QT, num_kv_heads);
+  size_t lds = (size_t)R * (dim + 8) * 2 + (size_t)R * (C + 1) * 4;
+  if (lds > 160 * 1024) return SBSA_ERR_UNSUPPORTED;
+  if (lds > 64 * 1024) {
+    hipFuncSetAttribute((const void*)score_select_kernel<64>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)score_select_kernel<128>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipFuncSetAttribute((const void*)score_select_kernel<256>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  }
+  switch (dim) {
+    case 64:
+      hipLaunchKernelGGL(score_select_kernel<64>, grid, dim3(256), lds, stream, a, R);
+      break;
+    case 128:
+      hipLaunchKernelGGL(score_select_kernel<128>, grid, dim3(256), lds, stream, a, R);
+      break;
+    case 256:
+      hipLaunchKernelGGL(score_select_kernel<256>, grid, dim3(256), lds, stream, a, R);
+      break;
+    default:
+      return SBSA_ERR_UNSUPPORTED;
+  }
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+int sbsa_causal_sizes(const int32_t* posting, int64_t width, const int32_t* indptr,
+                      const int32_t* sizes, int num_kv_heads, int num_clusters,
+                      int64_t pos_limit, int32_t* out, hipStream_t stream) {
+  if (!posting || !indptr || !sizes || !out || num_kv_heads < 1 || num_clusters < 1) return SBSA_ERR_ARG;
+  int n = num_kv_heads * num_clusters;
+  hipLaunchKernelGGL(causal_sizes_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, posting,
+                     width, indptr, sizes, num_kv_heads, num_clusters, pos_limit, out);
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+int sbsa_reverse_index(const int32_t* qmask, int num_queries, int num_kv_heads, int num_clusters,
+                       const int32_t* nvis, int32_t* rev_counts, int32_t* rev_indptr,
+                       int64_t* nnz, int32_t* qvals, int64_t qvals_cap, int32_t* qrank,
+                       hipStream_t stream) {
+  if (!qmask || !nvis || !rev_counts || !rev_indptr || !nnz || !qvals || !qrank) return SBSA_ERR_ARG;
+  if (num_clusters % 32 || num_clusters < 32 || num_queries < 0) return SBSA_ERR_ARG;
+  int64_t bound = (int64_t)num_queries * num_kv_heads * num_clusters;
+  if (qvals_cap < bound) return SBSA_ERR_CAPACITY;
+  int n = num_kv_heads * num_clusters;
+  hipLaunchKernelGGL(rev_pass_kernel, dim3(n), dim3(256), 0, stream, 0, qmask, num_queries,
+                     num_kv_heads, num_clusters, nvis, rev_counts, rev_indptr, qvals, qrank);
+  hipLaunchKernelGGL(rev_scan_kernel, dim3(1), dim3(1024), 0, stream, rev_counts, n, rev_indptr, nnz);
+  hipLaunchKernelGGL(rev_pass_kernel, dim3(n), dim3(256), 0, stream, 1, qmask, num_queries,
+                     num_kv_heads, num_clusters, nvis, rev_counts, rev_indptr, qvals, qrank);
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads, int num_clusters,
+                                 int queries_per_item) {
+  int64_t qt = queries_per_item;
+  return (int64_t)num_kv_heads * ((num_queries + qt - 1) / qt) +
+         (int64_t)num_kv_heads * num_clusters + (nnz + qt - 1) / qt;
+}
+
+int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
+                       int num_queries, int queries_per_item, int has_local, void* items,
+                       int64_t items_cap, int32_t* n_items, int32_t* counter, hipStream_t stream) {
+  if (!rev_counts || !items || !n_items || !counter || queries_per_item < 1) return SBSA_ERR_ARG;
+  hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), 0, stream, rev_counts, num_kv_heads,
+                     num_clusters, num_queries, queries_per_item, has_local, (int4*)items, n_items,
+                     counter, items_cap);
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+"""Paper defaults and the cluster-count rule of the flat partition.
+
+Values follow semblo/vllm_plugin/paper_defaults.py:42-104 (PAPER_ENV,
+PAPER_TEXT_CONFIG, budget K = capacity / 16) and state.py:586-597 (the
+power-of-two cluster count).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+PAGE = 16                    # SEMBLO_FA3_BODY / SEMBLO_FA3_ALIGN
+FLAT_UNIT_TOKENS = 2048      # SEMBLO_FLAT_UNIT_TOKENS
+FLAT_MIN_CLUSTERS_LOG2 = 7   # SEMBLO_FLAT_MIN_CLUSTERS_LOG2
+BUDGET_DIVISOR = 16          # K = L / 16
+CAPACITY_MULTIPLE = 16384
+
+
+def flat_cluster_count(length: int, target_size: int, *, min_clusters: int = 64,
+                       max_clusters: int = 16384) -> int:
+    """flat_index.py:81-84."""
+    return int(min(max(length // max(target_size, 1), min_clusters), max_clusters, length))
+
+
+def num_flat_clusters(length: int, unit_tokens: int = FLAT_UNIT_TOKENS,
+                      min_log2: int = FLAT_MIN_CLUSTERS_LOG2) -> int:
+    """state.py:586-597: a power of two, floored at 2^min_log2, capped by the prompt."""
+    min_c_log2 = max(3, int(min_log2))
+    raw = flat_cluster_count(length, unit_tokens)
+    c = 1 << max(min_c_log2, (max(raw, 1) - 1).bit_length())
+    return min(c, 1 << (int(length).bit_length() - 1))
+
+
+@dataclass
+class SembloRuntimeConfig:
+    """The settings of one sparse layer on the paper path (config.py:93-198 subset)."""
+
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    selection_temperature: float = 0.1      # paper (paper_defaults.py:89)
+    bucket_size_penalty: float = 0.25       # paper (paper_defaults.py:82)
+    query_chunk_size: int = 8192            # paper (paper_defaults.py:99)
+    target_tokens: int = 0                  # 0: L / 16
+    codebook_seed: int = 0
+    layer_idx: int = 0
+    flat_unit_tokens: int = FLAT_UNIT_TOKENS
+    flat_min_clusters_log2: int = FLAT_MIN_CLUSTERS_LOG2
+    page_align: int = PAGE
+    kmeans_sample_size: int = 8192
+    dense_prefix_x: int = 4                 # SEMBLO_FA3_DENSE_PREFIX_X
+    iters: int = 16
+    decode_num_splits: int = 64             # prompt splits of the decode step
+    decode_suffix_splits: int = 8           # SEMBLO_DECODE_SUFFIX_SPLITS
+    suffix_block: int = 256
+    suffix_reserve: int = 1024
+    sm_scale: float | None = None           # None: head_dim ** -0.5
+
+    @property
+    def scale(self) -> float:
+        return self.sm_scale if self.sm_scale is not None else self.head_dim ** -0.5
+
+    def budget(self, prompt_length: int) -> int:
+        return int(self.target_tokens) if self.target_tokens > 0 else max(1, prompt_length // BUDGET_DIVISOR)

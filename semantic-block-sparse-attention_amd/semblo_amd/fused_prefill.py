@@ -1,0 +1,119 @@
+"""Per-chunk prefill and the prompt part of a decode step (the reference's
+semblo/vllm_plugin/fused_prefill.py seams, paper path: FA3 page 16, KV-outer).
+
+  CausalSnapshot          cluster sizes at a position       (fused_prefill.py:44-135)
+  fused_chunk_attention   dense prefix or select + KV-outer (fused_prefill.py:219-482)
+  fused_decode_attention  one query over the packed prompt  (fused_prefill.py:625-718)
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .fused_select import theta_select_bitmask_flat
+from .kv_outer import dense_causal_attention, kv_outer_attention
+
+
+@dataclass(frozen=True)
+class PagedSparseAttentionResult:
+    """paged_attention.py:44-47."""
+
+    output: torch.Tensor             # [Q, Hq, D]
+    logsumexp: torch.Tensor | None   # [Q, Hq]
+
+
+class CausalSnapshot:
+    """Per-cluster counts of keys at positions <= p (fused_prefill.py:44-135).
+
+    Keys enter a cluster's run in position order, so the count at p is found
+    by a binary search in each run (one small kernel) instead of the
+    reference's running bincount.
+    """
+
+    def __init__(self, index) -> None:
+        self.index = index
+        self.length = int(index.prompt_length)
+        hkv, c = index.bucket_sizes.shape
+        self.sizes = torch.zeros(hkv, c, dtype=torch.int32, device=index.bucket_sizes.device)
+        self.next_pos = 0
+
+    def advance(self, last_pos: int) -> torch.Tensor:
+        """Counts at positions <= last_pos (calls must be non-decreasing)."""
+        hi = min(int(last_pos) + 1, self.length)
+        if hi > self.next_pos:
+            self.index.causal_sizes(hi, out=self.sizes)
+            self.next_pos = hi
+        return self.sizes
+
+
+def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor,
+                          snapshot_state: CausalSnapshot, chunk_start: int, chunk_end: int, *,
+                          temperature: float, beta: float, target_tokens: int,
+                          queries_per_block: int = 32, sm_scale: float, iters: int = 16,
+                          fa3_page_size: int = 16, kv_outer_default: bool = True,
+                          dense_prefix_x: int = 4, local: int = 0, out: torch.Tensor | None = None,
+                          **unused) -> torch.Tensor:
+    """Attention of one query chunk [chunk_start, chunk_end] (fused_prefill.py:219-482).
+
+    While chunk_start <= dense_prefix_x * K the chunk is dense and causal over
+    the whole prefix (fused_prefill.py:259-279); otherwise every cluster's
+    rows before wstart = chunk_start are read sparsely, per query, and the
+    chunk's own tokens through the exact causal window.
+    """
+    if not kv_outer_default or not fa3_page_size:
+        raise NotImplementedError("only the paper path (FA3 page body, KV-outer) is built")
+    q_count = q_chunk.shape[0]
+    hkv = index.num_kv_heads
+    c = index.num_buckets
+    cap = dense_prefix_x * target_tokens
+    wstart = 0 if chunk_start <= cap else max(0, chunk_start - local)
+    if index.original_kv is None:
+        raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
+                           "(index.original_kv), which this index no longer holds")
+    k_orig, v_orig = index.original_kv
+    if wstart == 0:
+        return dense_causal_attention(q_chunk, k_orig, v_orig, sm_scale=sm_scale,
+                                      chunk_start=chunk_start, out=out)
+    sizes = snapshot_state.advance(wstart - 1)
+    causal_sizes = sizes.clone()
+    vectors = query_state.vectors[0]
+    logmix = query_state.mixture_weights[0].float().clamp_min(1e-12).log()
+    g_union = min(queries_per_block, q_count)
+    nb = (q_count + g_union - 1) // g_union
+    bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
+    qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
+    theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None], bitmask,
+                              temperature=temperature, beta=beta, target_tokens=target_tokens,
+                              g_union=g_union, iters=iters, qmask=qmask)
+    window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
+    res, _ = kv_outer_attention(q_chunk, index.packed_kv, qmask, causal_sizes,
+                                index.bucket_indptr, sm_scale=sm_scale, page_size=fa3_page_size,
+                                aligned=True, local_kv=window, chunk_start=chunk_start,
+                                wstart=wstart, out=out)
+    return res
+
+
+def fused_decode_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor, *,
+                           temperature: float, beta: float, target_tokens: int, sm_scale: float,
+                           iters: int = 16, num_splits: int = 64,
+                           **unused) -> PagedSparseAttentionResult:
+    """One decode query over the packed prompt, selection against the full cluster
+    sizes (fused_prefill.py:625-718).  The generated suffix is merged by the caller."""
+    from .fused_decode import decode_prompt_only
+    return decode_prompt_only(q_chunk, query_state.vectors[0], index, temperature=temperature,
+                              beta=beta, target_tokens=target_tokens, sm_scale=sm_scale,
+                              iters=iters, num_splits=num_splits)
+
+
+def merge_paged_attention_results(left: PagedSparseAttentionResult,
+                                  right: PagedSparseAttentionResult) -> PagedSparseAttentionResult:
+    """Exact LSE merge of two disjoint key sets (paged_attention.py:50-80)."""
+    if left.logsumexp is None or right.logsumexp is None:
+        raise ValueError("attention-state merge requires logsumexp from both inputs")
+    merged = torch.logaddexp(left.logsumexp.float(), right.logsumexp.float())
+    wl = torch.exp(left.logsumexp.float() - merged)
+    wr = torch.exp(right.logsumexp.float() - merged)
+    out = (left.output.float() * wl.unsqueeze(-1) + right.output.float() * wr.unsqueeze(-1))
+    return PagedSparseAttentionResult(output=out.to(left.output.dtype), logsumexp=merged)

@@ -1,0 +1,158 @@
+"""KV-outer sparse prefill attention (S4 + S5 + S6) on HIP.
+
+The reference (semblo/vllm_plugin/kv_outer.py:482-816) builds a reverse index
+from each query's selected clusters, makes one FA3 varlen call per
+(cluster, KV head) whose query rows are the queries that picked it, one FA3
+call over the chunk's own causal window, and folds the partials per query by
+log-sum-exp.  Here the same three steps are three libsbsa calls:
+
+  sbsa_reverse_index    the CSR (query ids per (head, cluster)) and each
+                        query's rank in its clusters' lists     (kv_outer.py:254-329)
+  sbsa_prefill_items +  one persistent MFMA kernel over a work list of
+  sbsa_prefill_attend   (head, cluster | window, 128/G queries) items,
+                        partials in bf16 with their LSE        (kv_outer.py:661-753)
+  sbsa_prefill_combine  window first, then the clusters in order (kv_outer.py:370-479)
+
+One host read per call (the entry count, which sizes the partial buffer), as
+in the reference (kv_outer.py:604-613).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+ROWS_PER_ITEM = 128
+
+
+def queries_per_item(q_per_kv: int) -> int:
+    return ROWS_PER_ITEM // q_per_kv
+
+
+def default_grid(device: torch.device) -> int:
+    props = torch.cuda.get_device_properties(device)
+    return int(props.multi_processor_count) * 2
+
+
+def build_reverse_index(qmask: torch.Tensor, live: torch.Tensor, *, num_queries: int,
+                        block_q: int = 64, capacity=None):
+    """qmask [Q, H, C/32] int32, live [H, C] int32 (> 0: the cluster has visible rows).
+
+    Returns (qvals, counts [H, C], indptr [H*C + 1] int32, nnz (device int64),
+    qrank [Q, H, C] int32): qvals lists, per (head, cluster), the ascending
+    query ids that selected it; qrank[q, h, c] is q's place in that list.
+    """
+    q_all, hkv, nw = qmask.shape
+    c = nw * 32
+    dev = qmask.device
+    counts = torch.empty(hkv, c, dtype=torch.int32, device=dev)
+    indptr = torch.empty(hkv * c + 1, dtype=torch.int32, device=dev)
+    nnz = torch.empty(1, dtype=torch.int64, device=dev)
+    cap = max(num_queries * hkv * c, 1)
+    qvals = torch.empty(cap, dtype=torch.int32, device=dev)
+    qrank = torch.empty(num_queries, hkv, c, dtype=torch.int32, device=dev)
+    live32 = live if live.dtype == torch.int32 and live.is_contiguous() else live.to(torch.int32).contiguous()
+    _lib.call("sbsa_reverse_index", _lib.ptr(qmask), num_queries, hkv, c, _lib.ptr(live32),
+              _lib.ptr(counts), _lib.ptr(indptr), _lib.ptr(nnz), _lib.ptr(qvals), cap,
+              _lib.ptr(qrank), _lib.stream(dev))
+    return qvals, counts, indptr, nnz, qrank
+
+
+def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Tensor,
+                       causal_sizes: torch.Tensor, bucket_indptr: torch.Tensor, *, sm_scale: float,
+                       page_size: int = 16, aligned: bool = True, local_kv=None,
+                       chunk_start: int | None = None, wstart: int | None = None,
+                       out: torch.Tensor | None = None, want_stats: bool = False,
+                       grid: int | None = None, **unused):
+    """Attention with the cluster outside and its queries gathered (kv_outer.py:482-499).
+
+    q [Q, Hq, D] bf16; packed_kv [2, Lp, Hkv, D]; qmask [Q, Hkv, C/32];
+    causal_sizes [Hkv, C] (visible rows per cluster: every visible row of a
+    selected cluster precedes the chunk); bucket_indptr [Hkv, C+1];
+    local_kv = (k, v), each [n_local, Hkv, D], the prompt-order window whose
+    first row is position ``wstart`` and whose last is the chunk's last query.
+    Returns (out [Q, Hq, D], stats).
+    """
+    if not aligned:
+        raise NotImplementedError("the packed layout is always page-aligned (SEMBLO_FA3_ALIGN=16)")
+    if local_kv is None:
+        raise NotImplementedError("the KV-outer body always merges the chunk's causal window")
+    qn, hq, d = q.shape
+    hkv = packed_kv.shape[2]
+    g = hq // hkv
+    c = qmask.shape[2] * 32
+    dev = q.device
+    _lib.require_device(q, packed_kv, qmask, causal_sizes, bucket_indptr)
+    k_loc, v_loc = local_kv
+    n_local = k_loc.shape[0]
+    if wstart is None:
+        wstart = 0
+    if chunk_start is None:
+        chunk_start = wstart + n_local - qn
+    if n_local != chunk_start + qn - wstart:
+        raise ValueError("the local window must run from wstart to the chunk's last query")
+    if k_loc.stride() != v_loc.stride():
+        raise ValueError("the window's K and V must share a layout")
+    nvis = causal_sizes if causal_sizes.dtype == torch.int32 else causal_sizes.to(torch.int32)
+    nvis = nvis.contiguous()
+    qvals, counts, rev_indptr, nnz_d, qrank = build_reverse_index(qmask, nvis, num_queries=qn)
+    nnz = int(nnz_d.item())                       # the one host read of the chunk
+    part_o = torch.empty(max(nnz, 1), g, d, dtype=q.dtype, device=dev)
+    part_lse = torch.empty(max(nnz, 1), g, dtype=torch.float32, device=dev)
+    local_o = torch.empty_like(q)
+    local_lse = torch.empty(qn, hq, dtype=torch.float32, device=dev)
+    qt = queries_per_item(g)
+    bound = _lib.query("sbsa_prefill_items_bound", nnz, qn, hkv, c, qt)
+    items = torch.empty(max(bound, 1), 4, dtype=torch.int32, device=dev)
+    n_items = torch.empty(2, dtype=torch.int32, device=dev)
+    s = _lib.stream(dev)
+    _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(items), bound,
+              _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+    _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
+              _lib.ptr(packed_kv), packed_kv.shape[1], _lib.ptr(k_loc), _lib.ptr(v_loc),
+              k_loc.stride(0), k_loc.stride(1), _lib.ptr(bucket_indptr), _lib.ptr(nvis), c,
+              _lib.ptr(rev_indptr), _lib.ptr(qvals), _lib.ptr(items), _lib.ptr(n_items),
+              _lib.ptr(n_items[1:]), _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
+              local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), int(chunk_start),
+              int(wstart), float(sm_scale), int(grid or default_grid(dev)), s)
+    if out is None:
+        out = torch.empty_like(q)
+    _lib.call("sbsa_prefill_combine", _lib.ptr(qmask), _lib.ptr(nvis), _lib.ptr(rev_indptr),
+              _lib.ptr(qrank), _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
+              local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), _lib.ptr(out),
+              out.stride(0), out.stride(1), None, qn, hq, hkv, d, c, s)
+    stats = {"partials": nnz}
+    if want_stats:
+        stats["charged"] = int((counts.to(torch.int64) * nvis.to(torch.int64)).sum())
+        stats["kv_read"] = int(nvis.to(torch.int64).sum())
+    return out, stats
+
+
+def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, sm_scale: float,
+                           chunk_start: int = 0, out: torch.Tensor | None = None,
+                           grid: int | None = None) -> torch.Tensor:
+    """Exact causal attention of q (positions chunk_start..) over k/v rows 0..chunk_end
+    in prompt order (fused_prefill.py:155-189, the dense-prefix chunks)."""
+    qn, hq, d = q.shape
+    hkv = k.shape[1]
+    g = hq // hkv
+    dev = q.device
+    _lib.require_device(q, k, v)
+    if k.shape[0] < chunk_start + qn:
+        raise ValueError("k/v must cover every position up to the chunk's last query")
+    qt = queries_per_item(g)
+    zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
+    bound = hkv * ((qn + qt - 1) // qt) + 1
+    items = torch.empty(bound, 4, dtype=torch.int32, device=dev)
+    n_items = torch.empty(2, dtype=torch.int32, device=dev)
+    if out is None:
+        out = torch.empty_like(q)
+    s = _lib.stream(dev)
+    _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(items),
+              bound, _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+    _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
+              None, 0, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), None, None, 32, None,
+              None, _lib.ptr(items), _lib.ptr(n_items), _lib.ptr(n_items[1:]), None, None,
+              _lib.ptr(out), out.stride(0), out.stride(1), None, int(chunk_start), 0,
+              float(sm_scale), int(grid or default_grid(dev)), s)
+    return out

@@ -1,0 +1,132 @@
+"""The sparse attention layer behind ``semblo::attention`` (host orchestration).
+
+Mirrors the reference's SembloAttention paths that the operator reaches
+(semblo/vllm_plugin/model.py):
+
+  attention_forward        prefill of the whole prompt, or one decode step  (model.py:1169-1269)
+  _ingest_prompt_kv        index build, packed K/V                            (model.py:1301-1382)
+  _run_product_attention   the query-chunk loop                               (model.py:856-1008)
+  _full_graph_decode_step  the decode step over the arena                     (model.py:708-783)
+
+vLLM's metadata, paged cache and profiling branch are not part of this
+build: the layer keeps its own per-request state, and a call with more than
+one token starts a new request.
+"""
+from __future__ import annotations
+
+import torch
+
+from .arena import DecodeArena
+from .attention_op import register_layer
+from .config import SembloRuntimeConfig
+from .fused_decode import fused_decode_step
+from .fused_prefill import CausalSnapshot, fused_chunk_attention
+from .state import ProductPostingIndex
+from .trivial_router import trivial_router_vectors
+
+
+class SembloQueryState:
+    """Routing vectors [1, Q, Hq, 1, I] and mixture weights [1, Q, Hq, 1] (model.py:432-489)."""
+
+    def __init__(self, vectors: torch.Tensor, mixture_weights: torch.Tensor):
+        self.vectors = vectors
+        self.mixture_weights = mixture_weights
+        self.descriptor_vectors = None
+        self.descriptor_gamma = None
+
+
+class SembloAttention:
+    """One full-attention layer's sparse core."""
+
+    def __init__(self, config: SembloRuntimeConfig, layer_name: str | None = None) -> None:
+        self.runtime_config = config
+        self.num_heads = config.num_q_heads
+        self.num_kv_heads = config.num_kv_heads
+        self.head_dim = config.head_dim
+        self.scaling = config.scale
+        self.layer_idx = config.layer_idx
+        self.layer_name = layer_name or f"semblo.layer.{config.layer_idx}"
+        self.index: ProductPostingIndex | None = None
+        self.arena: DecodeArena | None = None
+        self.target_tokens = 0
+        register_layer(self.layer_name, self)
+
+    # -- routing (S0) ---------------------------------------------------------
+    def _query_state(self, q_pre: torch.Tensor) -> SembloQueryState:
+        vec = trivial_router_vectors(q_pre, 1)
+        q, h, d = vec.shape
+        ones = torch.ones(1, q, h, 1, dtype=torch.float32, device=vec.device)
+        return SembloQueryState(vec.view(1, q, h, 1, d), ones)
+
+    # -- prefill ----------------------------------------------------------------
+    def _ingest_prompt_kv(self, k_pre: torch.Tensor, k_post: torch.Tensor,
+                          v: torch.Tensor) -> ProductPostingIndex:
+        cfg = self.runtime_config
+        length = k_pre.shape[0]
+        if length < 128:
+            raise ValueError("sparse prefill requires at least 128 prompt tokens")
+        positions = torch.arange(length, device=k_pre.device)
+        index = ProductPostingIndex.build(
+            k_pre, positions, kmeans_sample_size=cfg.kmeans_sample_size,
+            codebook_seed=cfg.codebook_seed + cfg.layer_idx, flat_unit_tokens=cfg.flat_unit_tokens,
+            flat_min_clusters_log2=cfg.flat_min_clusters_log2, page_align=cfg.page_align,
+            router_pass=True)
+        index.pack_prompt_kv(k_post, v)
+        index.original_kv = (k_post, v)
+        return index
+
+    def prefill(self, q_post, q_pre, k_pre, k_post, v, output) -> torch.Tensor:
+        cfg = self.runtime_config
+        length = q_post.shape[0]
+        q = q_post.view(length, self.num_heads, self.head_dim)
+        qp = q_pre.view(length, self.num_heads, self.head_dim)
+        kp = k_pre.view(length, self.num_kv_heads, self.head_dim)
+        kk = k_post.view(length, self.num_kv_heads, self.head_dim)
+        vv = v.view(length, self.num_kv_heads, self.head_dim)
+        out = output.view(length, self.num_heads, self.head_dim)
+        index = self._ingest_prompt_kv(kp, kk, vv)
+        self.index = index
+        self.target_tokens = cfg.budget(length)
+        snapshot = CausalSnapshot(index)
+        step = cfg.query_chunk_size
+        for start in range(0, length, step):
+            end = min(length, start + step)
+            cap = cfg.dense_prefix_x * self.target_tokens
+            qs = None if start <= cap else self._query_state(qp[start:end])
+            fused_chunk_attention(
+                q[start:end], qs, index, None, snapshot, start, end - 1,
+                temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
+                target_tokens=self.target_tokens, sm_scale=self.scaling, iters=cfg.iters,
+                dense_prefix_x=cfg.dense_prefix_x, out=out[start:end])
+        index.original_kv = None
+        self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
+                                 suffix_splits=cfg.decode_suffix_splits)
+        return output
+
+    # -- decode -----------------------------------------------------------------
+    def decode(self, positions, q_post, q_pre, k_post, v, output) -> torch.Tensor:
+        if self.arena is None:
+            raise RuntimeError("decode before any prefill: the layer has no index")
+        cfg = self.runtime_config
+        fused_decode_step(self, self.arena, q_post=q_post, q_pre=q_pre, positions=positions,
+                          k_post=k_post, v_states=v, output=output,
+                          temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
+                          target_tokens=self.target_tokens, sm_scale=self.scaling,
+                          num_splits=cfg.decode_num_splits, iters=cfg.iters,
+                          suffix_splits=cfg.decode_suffix_splits)
+        return output
+
+    def attention_forward(self, positions, hidden_states, q_post, k_post, v_states, q_pre, k_pre,
+                          output) -> None:
+        """The operator's body (model.py:1169-1269): a prompt of T > 1 tokens starting at
+        position 0 is a prefill; a single token after the prompt is a decode step."""
+        t = q_post.shape[0]
+        if t > 1 or self.arena is None:
+            if k_post is None or v_states is None or k_pre is None:
+                raise RuntimeError("a prefill needs the layer's K/V and pre-RoPE keys")
+            self.prefill(q_post, q_pre, k_pre, k_post, v_states, output)
+        else:
+            pos = positions.reshape(-1)[:1]
+            if pos.dtype != torch.int32:
+                pos = pos.to(torch.int32)
+            self.decode(pos, q_post, q_pre, k_post, v_states, output)

@@ -1,0 +1,217 @@
+"""The per-prompt index: flat spherical k-means block build and the packed K/V.
+
+Host side of the reference's ``ProductPostingIndex`` on the flat paper path
+(semblo/vllm_plugin/state.py:477-1012), with every array op on the GPU
+through libsbsa:
+
+  key_space        router + routing space            (routing_map.py:35-64, flat_index.py:144-166)
+  kmeans_*         fit_flat_codebook                  (flat_index.py:193-289)
+  kmeans_assign    assign_flat_buckets                (flat_index.py:376-383)
+  bucket_layout    argsort/bincount + page alignment  (state.py:850-866, 44-84)
+  pack_kv          pack_prompt_kv                     (state.py:950-997)
+
+The random draws (the fit sample, the initial centroids and the restart rows
+of empty clusters) come from a CPU ``torch.Generator`` seeded with
+``codebook_seed``, in the reference's call order.  The reference draws on the
+keys' device; drawing on the CPU makes the partition independent of the
+device's RNG, and identical to the reference's own CPU build.  It costs one
+small host read of the cluster counts per k-means iteration, as the
+reference's ``empty.any()`` test does.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .config import num_flat_clusters
+
+PACK_ALIGN = 256
+
+
+@dataclass
+class ProductPostingIndex:
+    """Flat-partition index of one layer's prompt (state.py:372-475 fields)."""
+
+    codebooks: torch.Tensor            # [Hkv, 2, C, I/2] descriptors (key dtype)
+    posting_positions: torch.Tensor    # [Hkv, W] int32 packed row -> position
+    bucket_indptr: torch.Tensor        # [Hkv, C+1] int32 (page-aligned run starts)
+    bucket_sizes: torch.Tensor         # [Hkv, C] int32
+    prompt_length: int
+    max_position: int
+    flat_clusters: int
+    page_align: int
+    _inverse_positions: torch.Tensor   # [Hkv, L] int32 position -> packed row
+    packed_kv: torch.Tensor | None = None
+    original_kv: tuple | None = None   # prompt-order (k, v) [L, Hkv, D] while prefill runs
+    extras: dict = field(default_factory=dict)
+
+    @property
+    def num_kv_heads(self) -> int:
+        return int(self.codebooks.shape[0])
+
+    @property
+    def num_buckets(self) -> int:
+        return int(self.flat_clusters)
+
+    @property
+    def num_centroids(self) -> int:
+        return int(self.codebooks.shape[2])
+
+    @property
+    def is_flat(self) -> bool:
+        return True
+
+    @classmethod
+    def build(cls, product_keys: torch.Tensor, positions: torch.Tensor, *, num_centroids: int = 128,
+              kmeans_iters: int = 4, kmeans_sample_size: int = 8192,
+              codebook_seed: int | None = 0, quantizer: str = "product",
+              kmeans_init: str = "random", centroid_refiner=None, kmeans_preprocess: str = "none",
+              flat_unit_tokens: int = 2048, flat_min_clusters_log2: int = 7, page_align: int = 16,
+              descriptor_weight=None, descriptor_bias=None, descriptor_activation: str = "softplus",
+              layer_idx: int | None = None, router_pass: bool = False,
+              fit_iters: int | None = None, num_clusters: int | None = None
+              ) -> "ProductPostingIndex":
+        """Fit the flat codebook and the posting lists (state.py:477-542 contract).
+
+        ``product_keys`` [L, Hkv, I] bf16 are the key router's output (or, with
+        ``router_pass=True``, the pre-RoPE keys, normalised here first).
+        ``positions`` must be 0..L-1.  ``num_centroids``, ``kmeans_iters``,
+        ``quantizer`` and ``kmeans_init`` are accepted for signature parity;
+        the flat path uses ``SEMBLO_FLAT_FIT_ITERS`` (default 8) iterations and
+        32 sample points per centroid, as the reference does.
+        """
+        if product_keys.ndim != 3:
+            raise ValueError("product_keys must have shape [L,Hkv,I]")
+        length, hkv, index_dim = product_keys.shape
+        if positions.shape != (length,):
+            raise ValueError("positions must have shape [L]")
+        if length == 0:
+            raise ValueError("cannot build an index for an empty prompt")
+        _lib.require_device(product_keys)
+        if descriptor_weight is not None:
+            raise NotImplementedError("cluster descriptors are not part of the flat paper path")
+        unit = int(os.environ.get("SEMBLO_FLAT_UNIT_TOKENS", flat_unit_tokens))
+        if unit <= 0:
+            raise ValueError("the index needs the flat partition: set SEMBLO_FLAT_UNIT_TOKENS "
+                             "or semblo_flat_unit_tokens to the mean block size")
+        min_log2 = int(os.environ.get("SEMBLO_FLAT_MIN_CLUSTERS_LOG2", flat_min_clusters_log2))
+        c = num_clusters or int(os.environ.get("SEMBLO_FLAT_CLUSTERS", "0")) \
+            or num_flat_clusters(length, unit, min_log2)
+        iters = fit_iters if fit_iters is not None else int(os.environ.get("SEMBLO_FLAT_FIT_ITERS", "8"))
+        per_c = int(os.environ.get("SEMBLO_FLAT_FIT_PER_C", "32"))
+        align = int(os.environ.get("SEMBLO_FA3_ALIGN", page_align))
+        fit_n = min(length, max(int(kmeans_sample_size), per_c * c))
+        if fit_n < c:
+            raise ValueError("sample must be at least as large as num_clusters")
+        if c % 64 or c > 1024:
+            raise ValueError(f"{c} clusters: the kernels take a multiple of 64 up to 1024")
+        dev = product_keys.device
+        gen = torch.Generator()
+        gen.manual_seed(int(codebook_seed or 0))
+        s = _lib.stream(dev)
+        pk = product_keys if product_keys.stride(-1) == 1 else product_keys.contiguous()
+        if pk.dtype != torch.bfloat16:
+            raise ValueError("product_keys must be bfloat16")
+
+        space_f32 = torch.empty(length, index_dim, dtype=torch.float32, device=dev)
+        space_bf = torch.empty(length, index_dim, dtype=torch.bfloat16, device=dev)
+        cent_f32 = torch.empty(c, index_dim, dtype=torch.float32, device=dev)
+        cent_bf = torch.empty(c, index_dim, dtype=torch.bfloat16, device=dev)
+        sums = torch.empty(c, index_dim, dtype=torch.float32, device=dev)
+        counts = torch.empty(c, dtype=torch.int32, device=dev)
+        assign_s = torch.empty(fit_n, dtype=torch.int32, device=dev)
+        assign_all = torch.empty(length, dtype=torch.int32, device=dev)
+        cap = length + c * (max(align, 1) - 1)
+        posting_full = torch.empty(hkv, cap, dtype=torch.int32, device=dev)
+        inverse = torch.empty(hkv, length, dtype=torch.int32, device=dev)
+        sizes = torch.empty(hkv, c, dtype=torch.int32, device=dev)
+        indptr = torch.empty(hkv, c + 1, dtype=torch.int32, device=dev)
+        totals = torch.empty(hkv, dtype=torch.int32, device=dev)
+        codebooks = torch.empty(hkv, 2, c, index_dim // 2, dtype=product_keys.dtype, device=dev)
+        ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        counts_host = torch.empty(c, dtype=torch.int32, pin_memory=True)
+
+        for h in range(hkv):
+            kh = pk[:, h]
+            _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
+                      int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
+            # fit_flat_codebook: sample, init, iterations (flat_index.py:237-288)
+            perm = torch.randperm(length, generator=gen)
+            sample_idx = perm[:fit_n].to(torch.int32).to(dev, non_blocking=False)
+            init = torch.randperm(fit_n, generator=gen)[:c].to(torch.int32).to(dev)
+            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(space_f32),
+                      index_dim, _lib.ptr(sample_idx), c, index_dim, _lib.ptr(cent_f32),
+                      _lib.ptr(cent_bf), s)
+            for _ in range(iters):
+                _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, _lib.ptr(sample_idx),
+                          fit_n, _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_s), s)
+                _lib.call("sbsa_kmeans_update", _lib.ptr(space_f32), index_dim,
+                          _lib.ptr(sample_idx), fit_n, _lib.ptr(assign_s), c, index_dim,
+                          _lib.ptr(sums), _lib.ptr(counts), s)
+                counts_host.copy_(counts)          # one host read per iteration
+                torch.cuda.current_stream(dev).synchronize()
+                empty = counts_host == 0
+                src = torch.full((c,), -1, dtype=torch.int32)
+                n_empty = int(empty.sum())
+                if n_empty:
+                    repl = torch.randperm(fit_n, generator=gen)[:n_empty]
+                    src[empty] = repl.to(torch.int32)
+                src_d = src.to(dev)
+                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums), _lib.ptr(counts),
+                          _lib.ptr(src_d), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
+                          c, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+            # assign every key, lay the runs out, descriptor
+            _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, None, length,
+                      _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_all), s)
+            _lib.call("sbsa_bucket_layout", _lib.ptr(assign_all), length, c, max(align, 1),
+                      _lib.ptr(sizes[h]), _lib.ptr(indptr[h]), _lib.ptr(posting_full[h]), cap,
+                      _lib.ptr(inverse[h]), _lib.ptr(totals[h:h + 1]), _lib.ptr(ws), ws_bytes, s)
+            _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
+                      c, index_dim, None, _lib.ptr(codebooks[h]), s)
+        width = int(totals.max().item())
+        posting = posting_full[:, :width].contiguous()
+        return cls(codebooks=codebooks, posting_positions=posting, bucket_indptr=indptr,
+                   bucket_sizes=sizes, prompt_length=length, max_position=length - 1,
+                   flat_clusters=c, page_align=align if align > 1 else 0,
+                   _inverse_positions=inverse)
+
+    def pack_prompt_kv(self, key: torch.Tensor, value: torch.Tensor, *, pool=None) -> torch.Tensor:
+        """K/V in bucket order, [2, W padded to 256, Hkv, D] (state.py:950-997)."""
+        if key.shape != value.shape:
+            raise ValueError("key and value must have the same shape")
+        if key.ndim != 3 or key.shape[0] != self.prompt_length:
+            raise ValueError("key and value must have shape [L,Hkv,D]")
+        if key.shape[1] != self.num_kv_heads:
+            raise ValueError("key and value KV-head count differs from the index")
+        if key.stride() != value.stride() or key.stride(-1) != 1:
+            raise ValueError("key and value must share a row-major layout")
+        width = int(self.posting_positions.shape[1])
+        packed_len = width + (-width) % PACK_ALIGN
+        hkv, d = key.shape[1], key.shape[2]
+        shape = (2, packed_len, hkv, d)
+        packed = pool(shape, key.dtype, key.device) if pool is not None else \
+            torch.empty(shape, dtype=key.dtype, device=key.device)
+        _lib.call("sbsa_pack_kv", _lib.ptr(key), _lib.ptr(value), key.stride(0), key.stride(1),
+                  hkv, d, _lib.ptr(self.posting_positions), width, packed_len, _lib.ptr(packed),
+                  _lib.stream(key.device))
+        self.packed_kv = packed
+        return packed
+
+    def inverse_positions(self) -> torch.Tensor:
+        """[Hkv, L] int32: position -> packed row (state.py:999-1012)."""
+        return self._inverse_positions
+
+    def causal_sizes(self, pos_limit: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """[Hkv, C] keys of each cluster at positions < pos_limit."""
+        hkv, c = self.bucket_sizes.shape
+        if out is None:
+            out = torch.empty(hkv, c, dtype=torch.int32, device=self.bucket_sizes.device)
+        _lib.call("sbsa_causal_sizes", _lib.ptr(self.posting_positions),
+                  self.posting_positions.shape[1], _lib.ptr(self.bucket_indptr),
+                  _lib.ptr(self.bucket_sizes), hkv, c, int(pos_limit), _lib.ptr(out),
+                  _lib.stream(out.device))
+        return out

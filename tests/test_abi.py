@@ -1,0 +1,62 @@
+"""The C ABI: the library loads (no GPU needed) and exports what include/sbsa.h declares,
+with the argument counts the ctypes binding uses."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "sbsa.h"
+
+
+def _declarations():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"\b(int|size_t|int64_t)\s+(sbsa_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = [a.strip() for a in m.group(3).split(",") if a.strip() and a.strip() != "void"]
+        decls[m.group(2)] = len(args)
+    return decls
+
+
+def test_header_declares_the_entry_points():
+    decls = _declarations()
+    for name in ("sbsa_score_select", "sbsa_prefill_attend", "sbsa_decode_step",
+                 "sbsa_kmeans_assign", "sbsa_bucket_layout", "sbsa_reverse_index"):
+        assert name in decls
+
+
+def test_library_exports_every_declared_symbol():
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    lib = _lib.load()
+    decls = _declarations()
+    for name in decls:
+        assert hasattr(lib, name), name
+    for name, n in decls.items():
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+        assert len(_lib.SIGNATURES[name][1]) == n, f"{name}: header {n} args, binding {len(_lib.SIGNATURES[name][1])}"
+    assert lib.sbsa_abi_version() == 1
+
+
+def test_size_queries_run_without_a_gpu():
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    n = _lib.query("sbsa_decode_workspace_bytes", 16, 4, 128, 256, 64, 8)
+    assert n >= 16 * 72 * 256 * 4
+    assert _lib.query("sbsa_prefill_items_bound", 1000, 8192, 4, 128, 32) >= 1000 // 32
+    assert _lib.query("sbsa_bucket_layout_workspace_bytes", 131072, 128) >= 128 * 128 * 4
+
+
+def test_product_path_refuses_cpu_tensors():
+    import torch
+    from semblo_amd import _lib
+    from semblo_amd.trivial_router import trivial_router_vectors
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    with pytest.raises(RuntimeError):
+        trivial_router_vectors(torch.randn(4, 2, 64).to(torch.bfloat16))

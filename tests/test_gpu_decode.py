@@ -1,0 +1,145 @@
+"""S7-S9 on the GPU: the sparse decode step (suffix write, routing, selection against
+the full cluster sizes, split attention over the prompt CSR and the suffix, merge).
+
+Attention is checked against fp64 over exactly the selected clusters' rows plus
+the visible suffix (as tests/test_fused_decode_v3.py:98-124 of the reference
+does), selection against the oracle's up to near-ties, and the step captured
+in a HIP graph against the same steps run eagerly (bit-exact).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import assert_close_bf16, compare_selection, oracle_select
+from oracle import reference_cpu as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+class _Layer:
+    def __init__(self, hq, hkv, d):
+        self.num_heads, self.num_kv_heads, self.head_dim = hq, hkv, d
+
+
+def _setup(length, hq, hkv, d, seed, reserve=512, shuffle=True):
+    from semblo_amd.arena import DecodeArena
+    from semblo_amd.state import ProductPostingIndex
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(length, hq, hkv, d, mixtures=32, seg=(32, 256), seed=seed)
+    k, v = inp.k.to(DEV), inp.v.to(DEV)
+    idx = ProductPostingIndex.build(k, torch.arange(length, device=DEV), codebook_seed=seed,
+                                    router_pass=True)
+    idx.pack_prompt_kv(k, v)
+    gen = torch.Generator().manual_seed(seed) if shuffle else None
+    arena = DecodeArena(idx, reserve=reserve, shuffle_blocks=gen)
+    return inp, idx, arena
+
+
+def _csr_to_sel(csr, idx):
+    hkv, c = idx.bucket_sizes.shape
+    n = hkv * c
+    rstart = csr[:n].view(hkv, c)
+    rcount = csr[3 * n:3 * n + hkv]
+    indptr = idx.bucket_indptr.cpu()
+    sizes = idx.bucket_sizes.cpu()
+    sel = torch.zeros(hkv, c, dtype=torch.bool)
+    for h in range(hkv):
+        for p in range(int(rcount[h])):
+            st = int(rstart[h, p])
+            cand = torch.nonzero((indptr[h, :-1] == st) & (sizes[h] > 0)).flatten()
+            assert cand.numel() == 1
+            sel[h, cand[0]] = True
+    return sel
+
+
+@pytest.mark.parametrize("cfg", [dict(length=4096, hq=16, hkv=4, d=256, seed=1),
+                                 dict(length=3000, hq=8, hkv=2, d=128, seed=2)])
+def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
+    from semblo_amd.fused_decode import fused_decode_step
+    from semblo_amd.synthetic import decode_queries
+    length, hq, hkv, d = cfg["length"], cfg["hq"], cfg["hkv"], cfg["d"]
+    inp, idx, arena = _setup(length, hq, hkv, d, cfg["seed"])
+    steps = 40
+    qs, kn, vn = decode_queries(inp, steps, hq, seed=cfg["seed"])
+    layer = _Layer(hq, hkv, d)
+    target = length // 16
+    c = idx.num_buckets
+    csr = torch.empty(3 * hkv * c + 2 * hkv, dtype=torch.int32, device=DEV)
+    out = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(hq, dtype=torch.float32, device=DEV)
+    packed = idx.packed_kv.cpu()
+    near = 0
+    for t in range(steps):
+        pos = torch.tensor([length + t], dtype=torch.int32, device=DEV)
+        q = qs[t:t + 1].to(DEV)
+        fused_decode_step(layer, arena, q_post=q, q_pre=q, positions=pos, k_post=kn[t:t + 1].to(DEV),
+                          v_states=vn[t:t + 1].to(DEV), output=out, temperature=0.1, beta=0.25,
+                          target_tokens=target, sm_scale=d ** -0.5, num_splits=16, iters=16,
+                          out_lse=lse, csr_out=csr)
+        torch.cuda.synchronize()
+        sel = _csr_to_sel(csr.cpu(), idx)
+        want = ref.decode_reference(q[0].cpu(), packed, idx.bucket_indptr.cpu(),
+                                    idx.bucket_sizes.cpu(), sel, kn[:t + 1].cpu(), vn[:t + 1].cpu(),
+                                    d ** -0.5)
+        assert_close_bf16(out.view(hq, d).cpu(), want, f"step {t}")
+        vec = ref.trivial_router_vectors(q.cpu(), 1)
+        exp = oracle_select(vec, idx.codebooks.cpu(), idx.bucket_sizes.cpu()[None],
+                            temperature=0.1, beta=0.25, target=target)
+        rep = compare_selection(sel[None], exp["sel"], exp["score"], exp["theta"])
+        near += rep["near_ties"]
+        # the suffix store holds every generated token at its table slot
+        ks, vs = arena.suffix_rows(torch.arange(length, length + t + 1), 0)
+        assert torch.equal(ks.cpu(), kn[:t + 1, 0].cpu())
+    print(f"{cfg}: {steps} steps, {near} near-tie selection differences")
+
+
+def test_decode_step_replays_in_a_hip_graph():
+    from semblo_amd.fused_decode import fused_decode_step
+    from semblo_amd.synthetic import decode_queries
+    length, hq, hkv, d = 4096, 16, 4, 256
+    layer = _Layer(hq, hkv, d)
+    inp, idx_a, arena_a = _setup(length, hq, hkv, d, 5, shuffle=False)
+    _, idx_b, arena_b = _setup(length, hq, hkv, d, 5, shuffle=False)
+    steps = 12
+    qs, kn, vn = decode_queries(inp, steps, hq, seed=5)
+    kw = dict(temperature=0.1, beta=0.25, target_tokens=length // 16, sm_scale=d ** -0.5,
+              num_splits=32, iters=16)
+    # eager reference run
+    eager = []
+    out = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
+    for t in range(steps):
+        pos = torch.tensor([length + t], dtype=torch.int32, device=DEV)
+        fused_decode_step(layer, arena_a, q_post=qs[t:t + 1].to(DEV), q_pre=qs[t:t + 1].to(DEV),
+                          positions=pos, k_post=kn[t:t + 1].to(DEV), v_states=vn[t:t + 1].to(DEV),
+                          output=out, **kw)
+        eager.append(out.clone())
+    # captured run: static inputs, one capture, replays with eager work in between
+    s_q = torch.empty(1, hq, d, dtype=torch.bfloat16, device=DEV)
+    s_k = torch.empty(1, hkv, d, dtype=torch.bfloat16, device=DEV)
+    s_v = torch.empty(1, hkv, d, dtype=torch.bfloat16, device=DEV)
+    s_pos = torch.tensor([length], dtype=torch.int32, device=DEV)
+    s_out = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
+    s_q.copy_(qs[0:1])
+    s_k.copy_(kn[0:1])
+    s_v.copy_(vn[0:1])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):       # warm-up allocates the workspace outside the capture
+        fused_decode_step(layer, arena_b, q_post=s_q, q_pre=s_q, positions=s_pos, k_post=s_k,
+                          v_states=s_v, output=s_out, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fused_decode_step(layer, arena_b, q_post=s_q, q_pre=s_q, positions=s_pos, k_post=s_k,
+                          v_states=s_v, output=s_out, **kw)
+    for t in range(steps):
+        s_q.copy_(qs[t:t + 1])
+        s_k.copy_(kn[t:t + 1])
+        s_v.copy_(vn[t:t + 1])
+        s_pos.fill_(length + t)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(s_out, eager[t]), f"replay {t} differs from the eager step"

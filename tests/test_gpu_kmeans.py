@@ -1,0 +1,129 @@
+"""S1/S1b on the GPU: the flat k-means block build against the oracle (itself pinned
+bit-exact to the reference's ProductPostingIndex.build) and the reference's
+golden vectors.
+
+Both sides draw the same random rows (a CPU generator seeded alike), so the
+partition must match; a key may change cluster only as a near-tie of the bf16
+similarity argmax, which is counted and printed.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import reference_cpu as ref
+from synth import golden_keys
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+DEV = "cuda"
+
+
+def _build_gpu(product, **kw):
+    from semblo_amd.state import ProductPostingIndex
+    length = product.shape[0]
+    idx = ProductPostingIndex.build(product.to(DEV), torch.arange(length, device=DEV), **kw)
+    torch.cuda.synchronize()
+    return idx
+
+
+def _membership(posting, indptr, sizes):
+    """position -> cluster, [Hkv, L]."""
+    hkv, c = sizes.shape
+    length = int(sizes[0].sum())
+    out = torch.full((hkv, length), -1, dtype=torch.int64)
+    for h in range(hkv):
+        for cl in range(c):
+            s, n = int(indptr[h, cl]), int(sizes[h, cl])
+            out[h, posting[h, s:s + n].long()] = cl
+    return out
+
+
+def _check_index_invariants(idx, length):
+    sizes = idx.bucket_sizes.cpu()
+    indptr = idx.bucket_indptr.cpu()
+    posting = idx.posting_positions.cpu()
+    inverse = idx.inverse_positions().cpu()
+    hkv, c = sizes.shape
+    assert (sizes.sum(-1) == length).all()
+    assert ((indptr[:, 1:] - indptr[:, :-1]) % 16 == 0).all()
+    assert ((indptr[:, 1:] - indptr[:, :-1]) >= sizes).all()
+    for h in range(hkv):
+        seen = torch.zeros(length, dtype=torch.int64)
+        for cl in range(c):
+            s, n = int(indptr[h, cl]), int(sizes[h, cl])
+            run = posting[h, s:s + n].long()
+            assert (run[1:] > run[:-1]).all(), "a run is not in position order"
+            seen[run] += 1
+            assert torch.equal(inverse[h, run], torch.arange(s, s + n, dtype=torch.int32))
+        assert (seen == 1).all(), "every position in exactly one cluster"
+
+
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("kmeans_*.pt")))
+def test_build_matches_the_reference_golden(name):
+    g = torch.load(GOLDEN / name, weights_only=True)
+    length, hkv, d = int(g["length"]), int(g["hkv"]), int(g["d"])
+    k_pre = golden_keys(length, hkv, d, int(g["seed"]), mixture=name.endswith("_mix.pt"))
+    product = ref.routing_normalize_keys(k_pre)
+    idx = _build_gpu(product, codebook_seed=int(g["codebook_seed"]),
+                     flat_min_clusters_log2=int(g["min_log2"]))
+    _check_index_invariants(idx, length)
+    got = _membership(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(), idx.bucket_sizes.cpu())
+    want = _membership(g["posting"], g["indptr"], g["sizes"])
+    moved = int((got != want).sum())
+    print(f"{name}: {moved} of {got.numel()} keys in another cluster than the reference's")
+    assert moved <= max(2, got.numel() // 500)
+    if moved == 0:
+        assert torch.equal(idx.posting_positions.cpu(), g["posting"])
+        assert torch.equal(idx.bucket_indptr.cpu(), g["indptr"])
+        assert torch.equal(idx.inverse_positions().cpu(), g["inverse"])
+        cb = (idx.codebooks.cpu().float() - g["codebooks"].float()).abs()
+        assert float(cb.max()) <= 2 ** -8
+
+
+@pytest.mark.parametrize("length,hkv,d", [(8192, 2, 128), (16384, 4, 256)])
+def test_build_matches_the_oracle_on_mixture_keys(length, hkv, d):
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(length, hkv * 4, hkv, d, mixtures=64, seg=(32, 256), seed=length)
+    product = ref.routing_normalize_keys(inp.k)
+    want = ref.build_flat_index(product, codebook_seed=5)
+    idx = _build_gpu(product, codebook_seed=5)
+    _check_index_invariants(idx, length)
+    got_m = _membership(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(), idx.bucket_sizes.cpu())
+    want_m = _membership(want["posting"], want["indptr"], want["sizes"])
+    moved = int((got_m != want_m).sum())
+    print(f"L={length} Hkv={hkv} D={d}: {moved} of {got_m.numel()} keys moved (near-ties)")
+    assert moved <= max(2, got_m.numel() // 500)
+
+
+def test_router_pass_equals_building_from_router_output():
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(4096, 8, 2, 128, mixtures=32, seed=9)
+    a = _build_gpu(ref.routing_normalize_keys(inp.k), codebook_seed=1)
+    b = _build_gpu(inp.k, codebook_seed=1, router_pass=True)
+    ma = _membership(a.posting_positions.cpu(), a.bucket_indptr.cpu(), a.bucket_sizes.cpu())
+    mb = _membership(b.posting_positions.cpu(), b.bucket_indptr.cpu(), b.bucket_sizes.cpu())
+    assert int((ma != mb).sum()) <= 8
+
+
+def test_pack_gathers_through_the_posting_list():
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(2048, 8, 2, 128, mixtures=16, seed=4)
+    idx = _build_gpu(ref.routing_normalize_keys(inp.k), codebook_seed=0)
+    k, v = inp.k.to(DEV), inp.v.to(DEV)
+    packed = idx.pack_prompt_kv(k, v).cpu()
+    want = ref.pack_prompt_kv(idx.posting_positions.cpu(), inp.k, inp.v)
+    assert torch.equal(packed, want)
+
+
+def test_causal_sizes_match_the_snapshot_rule():
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(4096, 8, 2, 128, mixtures=16, seed=2)
+    idx = _build_gpu(ref.routing_normalize_keys(inp.k), codebook_seed=0)
+    for limit in (0, 1, 777, 2048, 4095, 4096):
+        got = idx.causal_sizes(limit).cpu()
+        want = ref.causal_sizes_at(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(),
+                                   idx.bucket_sizes.cpu(), limit)
+        assert torch.equal(got, want)

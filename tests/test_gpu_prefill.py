@@ -1,0 +1,148 @@
+"""S3c/S4/S5/S6 on the GPU: the KV-outer sparse prefill and the dense-prefix chunks.
+
+The attention is checked against an fp64 softmax over exactly the key set the
+reference defines for a query at position p in KV group h
+(kv_outer.py:482-816): the first causal_sizes[h, c] rows of every cluster c
+the query selected, plus positions wstart..p -- with the GPU's own selection,
+which is itself checked against the oracle's up to near-ties.  Tolerance:
+2e-2 abs + 1e-2 rel (bf16).
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_util import (assert_close_bf16, attention_reference, cluster_position_mask,
+                      compare_selection, oracle_select)
+from oracle import reference_cpu as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _setup(length, hq, hkv, d, seed, mixtures=32):
+    from semblo_amd.state import ProductPostingIndex
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(length, hq, hkv, d, mixtures=mixtures, seg=(32, 256), seed=seed)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    idx = ProductPostingIndex.build(k, torch.arange(length, device=DEV), codebook_seed=seed,
+                                    router_pass=True)
+    idx.pack_prompt_kv(k, v)
+    idx.original_kv = (k, v)
+    return inp, q, k, v, idx
+
+
+def _run_sparse_chunk(idx, q, k, v, cs, ce, target, *, tau=0.1, beta=0.25):
+    from semblo_amd.kv_outer import kv_outer_attention
+    from semblo_amd.fused_select import theta_select_bitmask_flat
+    from semblo_amd.trivial_router import trivial_router_vectors
+    hkv, c = idx.bucket_sizes.shape
+    qc = q[cs:ce + 1]
+    qn, hq, d = qc.shape
+    sizes = idx.causal_sizes(cs)
+    vec = trivial_router_vectors(qc, 1)
+    qmask = torch.empty(qn, hkv, c // 32, dtype=torch.int32, device=DEV)
+    theta = torch.empty(qn, hkv, dtype=torch.float32, device=DEV)
+    theta_select_bitmask_flat(vec.view(qn, hq, 1, d), None, idx.codebooks, sizes[None], None,
+                              temperature=tau, beta=beta, target_tokens=target, g_union=32,
+                              qmask=qmask, theta_out=theta)
+    out, stats = kv_outer_attention(qc, idx.packed_kv, qmask, sizes, idx.bucket_indptr,
+                                    sm_scale=d ** -0.5, local_kv=(k[cs:ce + 1], v[cs:ce + 1]),
+                                    chunk_start=cs, wstart=cs)
+    torch.cuda.synchronize()
+    return out.cpu(), qmask.cpu(), sizes.cpu(), vec.cpu(), theta.cpu()
+
+
+def _reference_sparse(idx, q, k, v, cs, ce, qmask, sizes):
+    hkv, c = sizes.shape
+    length = k.shape[0]
+    sel = ref.unpack_bits(qmask, c)                                   # [Qc, Hkv, C]
+    pos = cluster_position_mask(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(), sizes, length)
+    keys = torch.einsum("qhc,hcl->qhl", sel.double(), pos.double()) > 0
+    p = torch.arange(cs, ce + 1)
+    win = (torch.arange(length)[None, :] >= cs) & (torch.arange(length)[None, :] <= p[:, None])
+    keys |= win[:, None, :]
+    return attention_reference(q[cs:ce + 1].cpu(), keys, k.cpu(), v.cpu(), q.shape[-1] ** -0.5)
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(length=4096, hq=8, hkv=2, d=128, cs=2048, ce=3071, seed=1),
+    dict(length=2048, hq=16, hkv=4, d=256, cs=1024, ce=1535, seed=2),
+    dict(length=4096, hq=16, hkv=4, d=256, cs=3000, ce=3299, seed=3),     # ragged chunk
+    dict(length=3000, hq=4, hkv=4, d=128, cs=1900, ce=2999, seed=4),      # G = 1, odd length
+])
+def test_sparse_chunk_matches_fp64_over_the_selected_set(cfg):
+    inp, q, k, v, idx = _setup(cfg["length"], cfg["hq"], cfg["hkv"], cfg["d"], cfg["seed"])
+    target = cfg["length"] // 16
+    cs, ce = cfg["cs"], cfg["ce"]
+    out, qmask, sizes, vec, theta = _run_sparse_chunk(idx, q, k, v, cs, ce, target)
+    want = _reference_sparse(idx, q, k, v, cs, ce, qmask, sizes)
+    err = assert_close_bf16(out, want, f"sparse chunk {cfg}")
+    # the GPU's selection against the oracle's on the same index
+    exp = oracle_select(vec, idx.codebooks.cpu(), sizes[None], temperature=0.1, beta=0.25,
+                        target=target)
+    rep = compare_selection(ref.unpack_bits(qmask, sizes.shape[1]), exp["sel"], exp["score"],
+                            exp["theta"], theta)
+    print(f"{cfg}: max err {err:.3g}, selection {rep}")
+
+
+@pytest.mark.parametrize("cfg", [dict(length=2048, hq=8, hkv=2, d=128, cs=0, ce=1023),
+                                 dict(length=2048, hq=16, hkv=4, d=256, cs=512, ce=1300)])
+def test_dense_prefix_chunk_is_exact_causal_attention(cfg):
+    from semblo_amd.kv_outer import dense_causal_attention
+    from semblo_amd.synthetic import mixture_layer
+    inp = mixture_layer(cfg["length"], cfg["hq"], cfg["hkv"], cfg["d"], mixtures=8, seed=7)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    cs, ce = cfg["cs"], cfg["ce"]
+    out = dense_causal_attention(q[cs:ce + 1], k, v, sm_scale=cfg["d"] ** -0.5, chunk_start=cs).cpu()
+    p = torch.arange(cs, ce + 1)
+    keys = (torch.arange(cfg["length"])[None, :] <= p[:, None])[:, None, :].expand(-1, cfg["hkv"], -1)
+    want = attention_reference(inp.q[cs:ce + 1], keys, inp.k, inp.v, cfg["d"] ** -0.5)
+    err = assert_close_bf16(out, want, f"dense chunk {cfg}")
+    print(f"dense {cfg}: max err {err:.3g}")
+
+
+def test_layer_prefill_chunk_loop_through_the_operator():
+    """The whole-prompt path behind semblo::attention: build, pack, the chunk loop with
+    dense and sparse chunks; every chunk against fp64 over its key set."""
+    from semblo_amd.attention_op import sparse_attention_op
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.model import SembloAttention
+    from semblo_amd.synthetic import mixture_layer
+    length, hq, hkv, d = 4096, 8, 2, 128
+    cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=512,
+                              codebook_seed=3, layer_idx=0)
+    layer = SembloAttention(cfg, layer_name="test.prefill.0")
+    inp = mixture_layer(length, hq, hkv, d, mixtures=32, seed=11)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    positions = torch.arange(length, device=DEV)
+    out = torch.empty(length, hq * d, dtype=torch.bfloat16, device=DEV)
+    sparse_attention_op(positions, q.view(length, -1), q.view(length, -1), k, v, q, k, out,
+                        "test.prefill.0")
+    torch.cuda.synchronize()
+    got = out.view(length, hq, d).cpu()
+    idx = layer.index
+    target = length // 16
+    # chunks with start <= 4K are dense
+    for cs in range(0, length, 512):
+        ce = cs + 511
+        if cs <= 4 * target:
+            p = torch.arange(cs, ce + 1)
+            keys = (torch.arange(length)[None, :] <= p[:, None])[:, None, :].expand(-1, hkv, -1)
+        else:
+            sizes = idx.causal_sizes(cs).cpu()
+            vec = ref.trivial_router_vectors(inp.q[cs:ce + 1], 1)
+            sel = oracle_select(vec, idx.codebooks.cpu(), sizes[None], temperature=0.1,
+                                beta=0.25, target=target)["sel"]
+            pos = cluster_position_mask(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(),
+                                        sizes, length)
+            keys = torch.einsum("qhc,hcl->qhl", sel.double(), pos.double()) > 0
+            p = torch.arange(cs, ce + 1)
+            keys |= ((torch.arange(length)[None, :] >= cs)
+                     & (torch.arange(length)[None, :] <= p[:, None]))[:, None, :]
+        want = attention_reference(inp.q[cs:ce + 1], keys, inp.k, inp.v, d ** -0.5)
+        # near-tie selection differences move a handful of rows; compare per query
+        g = got[cs:ce + 1].double()
+        err = (g - want).abs() - (2e-2 + 1e-2 * want.abs())
+        bad_q = (err > 0).flatten(1).any(-1)
+        assert int(bad_q.sum()) <= 2, f"chunk {cs}: {int(bad_q.sum())} queries off"
