@@ -1,0 +1,296 @@
+"""Benchmark of the semantic block-sparse attention path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config 3] [--decode-steps N]
+
+Workload (the headline): one Qwen3.5-4B-shaped full-attention
+layer, a 131072-token prompt, 16 query heads / 4 KV heads / head_dim 256, bf16,
+synthetic Gaussian-mixture keys and queries (1024 centres, segment lengths
+log-uniform in [16, 2048], 4 sink tokens with 8x key norm), K = L/16 = 8192,
+query chunk 8192, paper selection settings (tau 0.1, beta 0.25).
+
+A step is one layer's prefill with the inputs resident in HBM: the semantic
+block build (spherical k-means per KV head), the packed K/V, and all 16 query
+chunks (5 dense-prefix chunks, 11 selected sparse chunks).  ``value`` is that
+time in ms per layer.  After the timed steps, the decode step is captured in a
+HIP graph N times in a row (256 steps, each with its own query and K/V) and the
+graph is replayed: ``decode_us_per_step``.
+
+``roofline`` is for the dominant kernel, the MFMA attention of the prefill:
+algorithmic FLOPs (4 D per selected key per query head, plus the causal window
+and the dense chunks) over its summed launch time from HIP events on its own
+stream.  ``decode_roofline`` is the decode step's algorithmic bytes over the
+per-step graph time.  ``cpu_baseline`` times the oracle's torch CPU path on a
+bounded sample of the same layer (see ``cpu_baseline`` below).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "semantic-block-sparse-attention_amd"))
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def _parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=None)
+    ap.add_argument("--decode-replays", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-queries", type=int, default=64)
+    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    return ap.parse_args()
+
+
+def _log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def run_prefill(layer, inp, timing=None):
+    from semblo_amd import kv_outer  # noqa: F401
+    length = inp.q.shape[0]
+    out = torch.empty(length, layer.num_heads * layer.head_dim, dtype=inp.q.dtype,
+                      device=inp.q.device)
+    layer.prefill(inp.q, inp.q, inp.k, inp.k, inp.v, out, timing=timing)
+    return out
+
+
+def decode_graph(layer, inp, steps, cfg):
+    """Capture `steps` consecutive decode steps in one HIP graph (each step reads its own
+    query, K/V and position from preloaded device buffers)."""
+    from semblo_amd.fused_decode import fused_decode_step
+    from semblo_amd.synthetic import decode_queries
+    length = inp.q.shape[0]
+    hq, hkv, d = layer.num_heads, layer.num_kv_heads, layer.head_dim
+    qs, kn, vn = decode_queries(inp, steps, hq, seed=11)
+    qs, kn, vn = qs.cuda(), kn.cuda(), vn.cuda()
+    pos = torch.arange(length, length + steps, dtype=torch.int32, device="cuda")
+    outs = torch.empty(steps, hq * d, dtype=torch.bfloat16, device="cuda")
+    kw = dict(temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
+              target_tokens=layer.target_tokens, sm_scale=layer.scaling,
+              num_splits=cfg.decode_num_splits, iters=cfg.iters,
+              suffix_splits=cfg.decode_suffix_splits)
+
+    def body():
+        for t in range(steps):
+            fused_decode_step(layer, layer.arena, q_post=qs[t:t + 1], q_pre=qs[t:t + 1],
+                              positions=pos[t:t + 1], k_post=kn[t:t + 1], v_states=vn[t:t + 1],
+                              output=outs[t:t + 1], **kw)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        body()                               # eager warm-up: workspace, every kernel once
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    return graph, outs
+
+
+def decode_bytes(layer, steps):
+    """Algorithmic HBM bytes of the captured steps: per step and KV head, the selected
+    rows' K and V (2 D bf16) and their position, the suffix rows visible so far, the
+    descriptors, and the query / output rows."""
+    from semblo_amd import _lib
+    idx = layer.index
+    hq, hkv, d = layer.num_heads, layer.num_kv_heads, layer.head_dim
+    c = idx.num_buckets
+    ws = layer.arena.fused_decode_ws.buffer
+    # the CSR of the last step: rtokens [Hkv] follows rstart, rlen, rcum, rcount
+    ints = ws.view(torch.int32)
+    rtok = ints[3 * hkv * c + hkv:3 * hkv * c + 2 * hkv].to(torch.int64).sum().item()
+    per_step_prompt = rtok * (2 * d * 2 + 4)
+    suffix = sum((t + 1) for t in range(steps)) / steps * hkv * 2 * d * 2
+    fixed = hkv * c * d * 2 + hq * d * 2 * 2
+    return per_step_prompt + suffix + fixed, rtok
+
+
+def cpu_baseline(inp, layer, cfg, sample_queries):
+    """The oracle's torch CPU path, timed on the host on a bounded sample.
+
+    Sample: the block build of one KV head over the whole prompt (scaled by Hkv),
+    and `sample_queries` queries of the last sparse chunk (selection + sparse
+    attention over their selected clusters and window, fp32), scaled to the
+    layer's query count.  The dense-prefix chunks are charged at the same
+    per-key rate as the sparse attention (keys per query x queries)."""
+    from oracle import reference_cpu as ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
+    length, hq, d = inp.q.shape
+    hkv = inp.k.shape[1]
+    g = hq // hkv
+    k_cpu = inp.k[:, :1].cpu()
+    t0 = time.perf_counter()
+    product = ref.routing_normalize_keys(k_cpu)
+    idx = ref.build_flat_index(product, codebook_seed=0)
+    build_s = (time.perf_counter() - t0) * hkv
+    # a sample of the last chunk: selection + attention, fp32
+    target = layer.target_tokens
+    cs = length - cfg.query_chunk_size
+    qs = inp.q[cs:cs + sample_queries].cpu()
+    k1 = inp.k[:, :1].cpu().float()
+    v1 = inp.v[:, :1].cpu().float()
+    t0 = time.perf_counter()
+    sizes = ref.causal_sizes_at(idx["posting"], idx["indptr"], idx["sizes"], cs)
+    vec = ref.trivial_router_vectors(qs[:, :g], 1)
+    prob = ref.mixture_probs(vec, None, idx["codebooks"], cfg.selection_temperature)
+    sel = ref.theta_select(prob, sizes[None], beta=cfg.bucket_size_penalty, target_tokens=target,
+                           g_union=prob.shape[0])["sel"]
+    keys_total = 0
+    for i in range(qs.shape[0]):
+        p = cs + i
+        rows = [idx["posting"][0, int(idx["indptr"][0, c]):int(idx["indptr"][0, c]) + int(sizes[0, c])].long()
+                for c in torch.nonzero(sel[i, 0]).flatten().tolist()]
+        rows.append(torch.arange(cs, p + 1))
+        pos = torch.cat(rows)
+        kk, vv = k1[pos, 0], v1[pos, 0]
+        s = (qs[i, :g].float() @ kk.T) * (d ** -0.5)
+        torch.softmax(s, dim=-1) @ vv
+        keys_total += pos.numel()
+    sample_s = time.perf_counter() - t0
+    per_key = sample_s / max(keys_total, 1)              # seconds per (query, key) for G heads
+    # keys per query over the layer: dense chunks p+1, sparse chunks ~ K + window
+    n_chunks = length // cfg.query_chunk_size
+    cap = cfg.dense_prefix_x * target
+    total_keys = 0
+    for ci in range(n_chunks):
+        c0 = ci * cfg.query_chunk_size
+        n = cfg.query_chunk_size
+        if c0 <= cap:
+            total_keys += n * c0 + n * (n + 1) // 2
+        else:
+            total_keys += n * (keys_total / qs.shape[0] - (sample_queries + 1) / 2) + n * (n + 1) // 2
+    attn_s = per_key * total_keys * hkv
+    total_ms = (build_s + attn_s) * 1000.0
+    return {"value": round(total_ms, 1), "unit": "ms/layer", "cores": threads, "kind": "port",
+            "sample": (f"oracle torch CPU path, fp32: block build of 1 of {hkv} KV heads over the "
+                       f"full {length}-token prompt (x{hkv}) and selection + sparse attention of "
+                       f"{sample_queries} queries x {g} heads of the last chunk (1 KV head), "
+                       f"extrapolated per attended key to all {length} queries and {hkv} KV heads"),
+            "build_ms": round(build_s * 1000.0, 1), "attention_ms": round(attn_s * 1000.0, 1)}
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import semblo_amd
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.kv_outer import KernelTiming
+    from semblo_amd.model import SembloAttention
+    from semblo_amd.synthetic import CONFIGS, mixture_layer
+    semblo_amd.load_library()
+    conf = CONFIGS[args.config]
+    length, hq, hkv, d = conf["length"], conf["hq"], conf["hkv"], conf["d"]
+    dsteps = args.decode_steps if args.decode_steps is not None else conf["decode_steps"]
+    _log(f"config {args.config}: L={length} Hq={hq} Hkv={hkv} D={d}")
+    inp = mixture_layer(length, hq, hkv, d, mixtures=conf["mixtures"], seg=conf["seg"],
+                        log_uniform=conf["log_uniform"], sinks=conf["sinks"], seed=0,
+                        dtype=torch.bfloat16, device="cuda")
+    cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                              query_chunk_size=conf["chunk"], suffix_reserve=max(1024, dsteps + 16))
+    layer = SembloAttention(cfg, layer_name="bench.layer")
+    result = {}
+    if args.only in ("all", "prefill"):
+        for i in range(args.warmup):
+            run_prefill(layer, inp)
+            torch.cuda.synchronize()
+            _log(f"warm-up {i} done")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run_prefill(layer, inp)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0 / max(args.steps, 1)
+        _log(f"prefill {ms:.2f} ms/layer")
+        # one instrumented pass: attention kernel time and FLOPs, and the build time
+        timing = KernelTiming()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        run_prefill(layer, inp, timing=timing)
+        ev[1].record()
+        torch.cuda.synchronize()
+        attn_ms = timing.total_ms()
+        flops = timing.total_flops()
+        achieved = flops / (attn_ms * 1e-3) / 1e12
+        result.update(prefill_ms=ms, attn_ms=attn_ms, flops=flops, achieved=achieved,
+                      launches=timing.launches())
+        _log(f"attention kernel {attn_ms:.2f} ms over {timing.launches()} launches, "
+             f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s")
+    if args.only in ("all", "decode"):
+        if layer.arena is None:
+            run_prefill(layer, inp)
+        graph, outs = decode_graph(layer, inp, dsteps, cfg)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.decode_replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / (args.decode_replays * dsteps)
+        nbytes, rtok = decode_bytes(layer, dsteps)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        result.update(decode_us=us, decode_bytes=nbytes, decode_gbs=gbs, decode_tokens=rtok)
+        _log(f"decode {us:.2f} us/step, {nbytes / 1e6:.1f} MB/step -> {gbs:.0f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline and args.only in ("all", "prefill"):
+        cpu = cpu_baseline(inp, layer, cfg, args.cpu_sample_queries)
+        _log(f"cpu baseline {cpu['value']} ms/layer on {cpu['cores']} threads")
+    line = {
+        "metric": "sparse prefill ms/layer @128K + decode us/step/layer; % MFMA / HBM roofline",
+        "value": round(result.get("prefill_ms", float("nan")), 3),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(result.get("prefill_ms", float("nan")), 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (Gaussian-mixture keys/queries, N(0,1) values, seeded)",
+        "config": {"workload": f"config {args.config}: one full-attention layer, L={length}, "
+                               f"Hq={hq}, Hkv={hkv}, D={d}, K={layer.target_tokens}, "
+                               f"chunk {conf['chunk']}, block build + 16-chunk sparse prefill; "
+                               f"{dsteps} hipGraph-captured decode steps",
+                   "prompt_tokens": length, "decode_steps": dsteps},
+        "decode_us_per_step": round(result["decode_us"], 3) if "decode_us" in result else None,
+        "roofline": None if "achieved" not in result else {
+            "bound": "mfma", "achieved": round(result["achieved"], 1), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(result["achieved"] / PEAK_BF16_TFLOPS, 4),
+            "traffic": None, "kernel": "attn_items_kernel<256,4>",
+            "flops_per_layer": result["flops"], "kernel_ms_per_layer": round(result["attn_ms"], 3),
+            "launches_per_layer": result["launches"]},
+        "decode_roofline": None if "decode_us" not in result else {
+            "bound": "hbm", "achieved": round(result["decode_gbs"], 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(result["decode_gbs"] / PEAK_HBM_GBS, 4),
+            "traffic": None, "bytes_per_step": result["decode_bytes"],
+            "selected_rows_per_step": result["decode_tokens"],
+            "scope": "whole step (select + attend + merge) from graph replay time"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -54,7 +54,7 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
                           queries_per_block: int = 32, sm_scale: float, iters: int = 16,
                           fa3_page_size: int = 16, kv_outer_default: bool = True,
                           dense_prefix_x: int = 4, local: int = 0, out: torch.Tensor | None = None,
-                          **unused) -> torch.Tensor:
+                          timing=None, **unused) -> torch.Tensor:
     """Attention of one query chunk [chunk_start, chunk_end] (fused_prefill.py:219-482).
 
     While chunk_start <= dense_prefix_x * K the chunk is dense and causal over
@@ -73,9 +73,15 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
         raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
                            "(index.original_kv), which this index no longer holds")
     k_orig, v_orig = index.original_kv
+    hq, d = q_chunk.shape[1], q_chunk.shape[2]
     if wstart == 0:
+        if timing is not None:
+            # sum over p in the chunk of (p + 1) keys, every query head, 4 D FLOPs per key
+            n = q_count
+            keys = n * (chunk_start + 1) + n * (n - 1) // 2
+            timing.add_flops(4.0 * d * hq * keys)
         return dense_causal_attention(q_chunk, k_orig, v_orig, sm_scale=sm_scale,
-                                      chunk_start=chunk_start, out=out)
+                                      chunk_start=chunk_start, out=out, timing=timing)
     sizes = snapshot_state.advance(wstart - 1)
     causal_sizes = sizes.clone()
     vectors = query_state.vectors[0]
@@ -84,14 +90,21 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     nb = (q_count + g_union - 1) // g_union
     bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
     qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
-    theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None], bitmask,
-                              temperature=temperature, beta=beta, target_tokens=target_tokens,
-                              g_union=g_union, iters=iters, qmask=qmask)
+    _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None],
+                                          bitmask, temperature=temperature, beta=beta,
+                                          target_tokens=target_tokens, g_union=g_union,
+                                          iters=iters, qmask=qmask)
+    if timing is not None:
+        # selected rows of every (query, KV head), each read by its G query heads,
+        # plus the causal window (p - chunk_start + 1 keys per query and head)
+        g = hq // hkv
+        window = q_count * (q_count + 1) // 2
+        timing.add_flops(4.0 * d * (g * tokens.to(torch.float64).sum() + hq * window))
     window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
     res, _ = kv_outer_attention(q_chunk, index.packed_kv, qmask, causal_sizes,
                                 index.bucket_indptr, sm_scale=sm_scale, page_size=fa3_page_size,
                                 aligned=True, local_kv=window, chunk_start=chunk_start,
-                                wstart=wstart, out=out)
+                                wstart=wstart, out=out, timing=timing)
     return res
 
 

@@ -63,7 +63,7 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
                        page_size: int = 16, aligned: bool = True, local_kv=None,
                        chunk_start: int | None = None, wstart: int | None = None,
                        out: torch.Tensor | None = None, want_stats: bool = False,
-                       grid: int | None = None, **unused):
+                       grid: int | None = None, timing=None, **unused):
     """Attention with the cluster outside and its queries gathered (kv_outer.py:482-499).
 
     q [Q, Hq, D] bf16; packed_kv [2, Lp, Hkv, D]; qmask [Q, Hkv, C/32];
@@ -108,6 +108,8 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(items), bound,
               _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+    if timing is not None:
+        timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               _lib.ptr(packed_kv), packed_kv.shape[1], _lib.ptr(k_loc), _lib.ptr(v_loc),
               k_loc.stride(0), k_loc.stride(1), _lib.ptr(bucket_indptr), _lib.ptr(nvis), c,
@@ -115,6 +117,8 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
               _lib.ptr(n_items[1:]), _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
               local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), int(chunk_start),
               int(wstart), float(sm_scale), int(grid or default_grid(dev)), s)
+    if timing is not None:
+        timing.end(s)
     if out is None:
         out = torch.empty_like(q)
     _lib.call("sbsa_prefill_combine", _lib.ptr(qmask), _lib.ptr(nvis), _lib.ptr(rev_indptr),
@@ -130,7 +134,7 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
 
 def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, sm_scale: float,
                            chunk_start: int = 0, out: torch.Tensor | None = None,
-                           grid: int | None = None) -> torch.Tensor:
+                           grid: int | None = None, timing=None) -> torch.Tensor:
     """Exact causal attention of q (positions chunk_start..) over k/v rows 0..chunk_end
     in prompt order (fused_prefill.py:155-189, the dense-prefix chunks)."""
     qn, hq, d = q.shape
@@ -150,9 +154,49 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(items),
               bound, _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+    if timing is not None:
+        timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               None, 0, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), None, None, 32, None,
               None, _lib.ptr(items), _lib.ptr(n_items), _lib.ptr(n_items[1:]), None, None,
               _lib.ptr(out), out.stride(0), out.stride(1), None, int(chunk_start), 0,
               float(sm_scale), int(grid or default_grid(dev)), s)
+    if timing is not None:
+        timing.end(s)
     return out
+
+
+class KernelTiming:
+    """HIP events around each launch of the attention kernel, on the stream it runs on.
+
+    ``begin``/``end`` bracket one launch; ``flops`` collects the algorithmic
+    FLOPs of each launch as device scalars (summed once, at read-out)."""
+
+    def __init__(self) -> None:
+        self.events: list[tuple] = []
+        self.flops: list = []
+
+    def begin(self, stream_handle: int) -> None:
+        # the kernels launch on torch's current stream (the handle passed to libsbsa)
+        assert stream_handle == torch.cuda.current_stream().cuda_stream
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events.append([ev, None])
+
+    def end(self, stream_handle: int) -> None:
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events[-1][1] = ev
+
+    def add_flops(self, value) -> None:
+        self.flops.append(value)
+
+    def launches(self) -> int:
+        return len(self.events)
+
+    def total_ms(self) -> float:
+        torch.cuda.synchronize()
+        return float(sum(a.elapsed_time(b) for a, b in self.events))
+
+    def total_flops(self) -> float:
+        return float(sum(float(f) for f in self.flops))

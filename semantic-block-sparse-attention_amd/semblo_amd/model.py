@@ -75,7 +75,7 @@ class SembloAttention:
         index.original_kv = (k_post, v)
         return index
 
-    def prefill(self, q_post, q_pre, k_pre, k_post, v, output) -> torch.Tensor:
+    def prefill(self, q_post, q_pre, k_pre, k_post, v, output, timing=None) -> torch.Tensor:
         cfg = self.runtime_config
         length = q_post.shape[0]
         q = q_post.view(length, self.num_heads, self.head_dim)
@@ -97,7 +97,7 @@ class SembloAttention:
                 q[start:end], qs, index, None, snapshot, start, end - 1,
                 temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
                 target_tokens=self.target_tokens, sm_scale=self.scaling, iters=cfg.iters,
-                dense_prefix_x=cfg.dense_prefix_x, out=out[start:end])
+                dense_prefix_x=cfg.dense_prefix_x, out=out[start:end], timing=timing)
         index.original_kv = None
         self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
                                  suffix_splits=cfg.decode_suffix_splits)

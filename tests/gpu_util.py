@@ -92,6 +92,32 @@ def cluster_position_mask(posting: torch.Tensor, indptr: torch.Tensor, counts: t
     return m
 
 
-def oracle_select(vectors, codebooks, sizes, *, temperature, beta, target, g_union=1):
+def oracle_select(vectors, codebooks, sizes, *, temperature, beta, target, g_union=None):
+    """The oracle's scores and bisection; one size snapshot ([1, Hkv, C]) serves every query."""
     prob = ref.mixture_probs(vectors.cpu(), None, codebooks.cpu(), temperature)
-    return ref.theta_select(prob, sizes.cpu(), beta=beta, target_tokens=target, g_union=g_union)
+    if g_union is None:
+        g_union = prob.shape[0] if sizes.shape[0] == 1 else 1
+    return ref.theta_select(prob, sizes.cpu(), beta=beta, target_tokens=target, g_union=max(g_union, 1))
+
+
+def membership_near_ties(product: torch.Tensor, codebooks: torch.Tensor, got: torch.Tensor,
+                         want: torch.Tensor) -> tuple[int, float]:
+    """Keys whose cluster differs between two builds: check each is a near-tie of the bf16
+    similarity argmax under the reference build's centroids.  The similarities are bf16
+    values, so a tie is resolved at bf16 resolution: the two clusters' fp32 similarities must
+    lie within two bf16 ulps (2^-7 relative) of each other.  Returns (moved, worst gap / ulp).
+    """
+    moved = torch.nonzero(got != want)
+    if moved.numel() == 0:
+        return 0, 0.0
+    space = torch.nn.functional.normalize(product.float(), dim=-1)
+    worst = 0.0
+    for h, pos in moved.tolist():
+        cent = torch.cat([codebooks[h, 0], codebooks[h, 1]], dim=-1).float()
+        x = space[pos, h].to(torch.bfloat16).double()
+        s_want = float(x @ cent[want[h, pos]].double())
+        s_got = float(x @ cent[got[h, pos]].double())
+        ulp = 2.0 ** -8 * max(abs(s_want), abs(s_got), 1e-6)
+        worst = max(worst, abs(s_want - s_got) / ulp)
+    assert worst <= 2.0, f"a moved key is not a near-tie: similarity gap {worst:.2f} bf16 ulps"
+    return int(moved.shape[0]), worst
