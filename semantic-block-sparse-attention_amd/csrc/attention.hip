@@ -46,22 +46,64 @@ struct AttnArgs {
 };
 
 constexpr int KT = 64;      // keys per tile
+// A row's running maximum is only raised (and the accumulators rescaled) when
+// a tile's maximum exceeds it by more than this (log2 units): probabilities
+// stay below 2^8, and most tiles skip the rescale of the accumulators.
+constexpr float RESCALE_LOG2 = 8.0f;
+constexpr int BUFFER_CONFIG = 0x00020000;   // raw buffer resource, 32-bit data format
+
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// LDS tile layout: K and V rows of D bf16, row-major; the 16-byte chunks of
+// row r are permuted by an XOR (K: chunk ^ (r % 8), V: chunk ^ 2 (r % 4)) so
+// that the MFMA operand reads hit distinct banks.  Tiles are filled straight
+// from global memory by buffer loads into LDS (lane l writes slot l of a 1 KB
+// run; rows past the item's last key are out of the buffer's range and read
+// as zero).
+template <int D>
+struct AttnTileShape {
+  static constexpr int CH = D / 8;                    // 16-byte chunks per row
+  static constexpr int ROW_BYTES = D * 2;
+  static constexpr int TILE_BYTES = KT * ROW_BYTES;   // one of K or V
+  static constexpr int BUF_BYTES = 2 * TILE_BYTES;    // K then V
+  static constexpr size_t LDS_BYTES = 2 * (size_t)BUF_BYTES;
+  static constexpr int ROWS_PER_INST = 64 / CH;       // rows one wave instruction covers
+  static constexpr int INSTS = KT / ROWS_PER_INST;    // instructions per K (or V) tile
+  static constexpr int PER_WAVE = INSTS / 4;
+};
 
 template <int D, int G>
 __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
+  using S = AttnTileShape<D>;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
-  constexpr int LDK = D + 8;
-  constexpr int LDV = KT + 4;
-  constexpr int DPT = D / 16;            // V dims per thread in the transposing load
-  __shared__ __attribute__((aligned(16))) bf16_t sK[KT * LDK];
-  __shared__ __attribute__((aligned(16))) bf16_t sV[D * LDV];
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
   __shared__ int s_item;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int total = *a.n_items;
   const float NEG_INF = -INFINITY;
+
+  // --- per-lane address bases (fixed for the kernel) ---------------------
+  // loads: instruction m of this wave covers rows r0 + m * 4 * ROWS_PER_INST
+  const int r0 = wave * S::ROWS_PER_INST + lane / S::CH;
+  const int cpos = lane % S::CH;
+  const uint32_t kslot = (uint32_t)((cpos ^ (r0 & 7)) * 16);          // (r0 + 4k*RPI) & 7 == r0 & 7
+  const uint32_t vslot = (uint32_t)((cpos ^ ((r0 & 3) << 1)) * 16);
+  // K operand reads: row kb*16 + l16, chunk (s*4 + lg) ^ (l16 & 7)
+  const int xb = (l16 >> 2) & 1, xl = l16 & 3;
+  const int kbase_even = l16 * S::ROW_BYTES + 64 * xb + 16 * (lg ^ xl);
+  const int kbase_odd = l16 * S::ROW_BYTES - 64 * xb + 16 * (lg ^ xl);
+  // V^T operand (transposing reads): row t2*32 + hlf*16 + lg*4 + (l16 >> 2),
+  // dims db*16 + (l16 & 3)*4 .. +4, chunk 2 (db ^ z) + b with z = (l16 >> 2) & 3
+  const int z = (l16 >> 2) & 3;
+  int vbase[4];
+#pragma unroll
+  for (int dl = 0; dl < 4; ++dl)
+    vbase[dl] = (lg * 4 + (l16 >> 2)) * S::ROW_BYTES + 32 * (dl ^ z) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
 
   while (true) {
     if (threadIdx.x == 0) s_item = atomicAdd(a.counter, 1);
@@ -83,13 +125,35 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       rs = a.o_st;
       nkeys = (int)(a.chunk_start + qb + qn - a.wstart);
     } else {
-      int64_t r0 = a.indptr[h * (a.C + 1) + c];
-      kp = a.packed + r0 * a.Hkv * D + (int64_t)h * D;
+      int64_t r0g = a.indptr[h * (a.C + 1) + c];
+      kp = a.packed + r0g * a.Hkv * D + (int64_t)h * D;
       vp = kp + a.packed_len * a.Hkv * D;
       rs = (int64_t)a.Hkv * D;
       nkeys = a.nvis[h * a.C + c];
       entry0 = (int64_t)a.rev_indptr[h * a.C + c] + qb;
     }
+    if (nkeys <= 0) continue;
+    const uint32_t rs_bytes = (uint32_t)(rs * 2);
+    const uint32_t kvoff = (uint32_t)r0 * rs_bytes;
+
+    // direct loads of tile t0 into buffer `buf`
+    auto issue_tile = [&](int t0, int buf) {
+      const uint32_t valid = (uint32_t)(nkeys - t0) * rs_bytes;   // rows past the item read 0
+      __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(kp + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
+      __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(vp + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
+      unsigned char* kdst = smem_attn + buf * S::BUF_BYTES + wave * 1024;
+      unsigned char* vdst = kdst + S::TILE_BYTES;
+#pragma unroll
+      for (int m = 0; m < S::PER_WAVE; ++m) {
+        const uint32_t roff = kvoff + (uint32_t)(m * 4 * S::ROWS_PER_INST) * rs_bytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(kdst + m * 4096), 16, roff + kslot, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(vdst + m * 4096), 16, roff + vslot, 0, 0, 0);
+      }
+    };
+
+    issue_tile(0, 0);   // in flight while the queries load
 
     // Q rows of this wave: R = wave*32 + rb*16 + l16 -> (slot i, head j)
     u32x4_t qr[2][KS];
@@ -109,6 +173,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       for (int s = 0; s < KS; ++s)
         qr[rb][s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
     }
+    // the last key any row of this wave may see
+    int wave_lim = max(qlim[0], qlim[1]);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
 
     f32x4_t o[DB][2];
 #pragma unroll
@@ -119,122 +187,110 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     float m_run[2] = {NEG_INF, NEG_INF};
     float l_run[2] = {0.f, 0.f};
 
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int cur = 0;
     for (int t0 = 0; t0 < nkeys; t0 += KT) {
-      // K tile: row-major, padded rows
-#pragma unroll
-      for (int k = 0; k < (KT * D / 8) / 256; ++k) {
-        const int e = threadIdx.x + 256 * k;
-        const int r = e / (D / 8), ch = e % (D / 8);
-        u32x4_t v = u32x4_t{0, 0, 0, 0};
-        if (t0 + r < nkeys) v = *reinterpret_cast<const u32x4_t*>(kp + (int64_t)(t0 + r) * rs + ch * 8);
-        *reinterpret_cast<u32x4_t*>(&sK[r * LDK + ch * 8]) = v;
-      }
-      // V tile transposed: thread -> keys 4kq..4kq+3, dims dc*DPT..+DPT
-      {
-        const int kq = threadIdx.x & 15, dc = threadIdx.x >> 4;
-        bf16_t vv[4][DPT];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const int key = t0 + kq * 4 + kk;
-          const bool ok = key < nkeys;
-          const bf16_t* src = vp + (int64_t)key * rs + dc * DPT;
-          if constexpr (DPT % 8 == 0) {
-#pragma unroll
-            for (int u = 0; u < DPT / 8; ++u) {
-              u32x4_t w = ok ? *reinterpret_cast<const u32x4_t*>(src + u * 8) : u32x4_t{0, 0, 0, 0};
-              __builtin_memcpy(&vv[kk][u * 8], &w, 16);
-            }
-          } else {
-            u32x2_t w = ok ? *reinterpret_cast<const u32x2_t*>(src) : u32x2_t{0, 0};
-            __builtin_memcpy(&vv[kk][0], &w, 8);
-          }
-        }
-#pragma unroll
-        for (int dd = 0; dd < DPT; ++dd) {
-          u32x2_t w;
-          w.x = (uint32_t)vv[0][dd] | ((uint32_t)vv[1][dd] << 16);
-          w.y = (uint32_t)vv[2][dd] | ((uint32_t)vv[3][dd] << 16);
-          *reinterpret_cast<u32x2_t*>(&sV[(dc * DPT + dd) * LDV + kq * 4]) = w;
-        }
-      }
-      __syncthreads();
+      const bool more = t0 + KT < nkeys;
+      if (more) issue_tile(t0 + KT, cur ^ 1);   // streams in during these MFMAs
+      const unsigned char* sK = smem_attn + cur * S::BUF_BYTES;
+      const unsigned char* sV = sK + S::TILE_BYTES;
 
-      // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of row (rb, l16)
-      f32x4_t sacc[4][2];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sacc[kb][0] = f32x4_t{0, 0, 0, 0};
-        sacc[kb][1] = f32x4_t{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
+      if (t0 <= wave_lim) {
+        // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of row (rb, l16)
+        f32x4_t sacc[4][2];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          u32x4_t ka = *reinterpret_cast<const u32x4_t*>(&sK[(kb * 16 + l16) * LDK + s * 32 + lg * 8]);
-          sacc[kb][0] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[0][s]), sacc[kb][0]);
-          sacc[kb][1] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[1][s]), sacc[kb][1]);
+          sacc[kb][0] = f32x4_t{0, 0, 0, 0};
+          sacc[kb][1] = f32x4_t{0, 0, 0, 0};
         }
-      }
-
-      // online softmax in the log2 domain
-      u32x4_t pb[2][2];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        float mx = NEG_INF;
+        for (int s = 0; s < KS; ++s) {
+          const unsigned char* kb0 = sK + ((s & 1) ? kbase_odd : kbase_even) + 64 * s;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = t0 + kb * 16 + lg * 4 + i;
-            float v = sacc[kb][rb][i] * a.scale_log2;
-            v = (key < nkeys && key <= qlim[rb]) ? v : NEG_INF;
-            sacc[kb][rb][i] = v;
-            mx = fmaxf(mx, v);
+          for (int kb = 0; kb < 4; ++kb) {
+            u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * S::ROW_BYTES);
+            sacc[kb][0] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[0][s]), sacc[kb][0]);
+            sacc[kb][1] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[1][s]), sacc[kb][1]);
           }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run[rb], mx);
-        const float m_use = (m_new == NEG_INF) ? 0.f : m_new;
-        const float alpha = exp2f(m_run[rb] - m_use);
-        float sum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float p = exp2f(sacc[kb][rb][i] - m_use);
-            sacc[kb][rb][i] = p;
-            sum += p;
-          }
-        sum += __shfl_xor(sum, 16, 64);
-        sum += __shfl_xor(sum, 32, 64);
-        l_run[rb] = l_run[rb] * alpha + sum;
-        m_run[rb] = m_new;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db][rb] *= alpha;
-        // B operand of P^T for key pairs (2t2, 2t2+1)
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
-          pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
-          pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
-          pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
         }
-      }
 
-      // O^T += V^T P^T
+        // online softmax in the log2 domain, with a lazily raised maximum
+        u32x4_t pb[2][2];
+        float alpha[2];
+        bool need_any = false;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+        for (int rb = 0; rb < 2; ++rb) {
+          float mx = NEG_INF;
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          const bf16_t* vrow = &sV[(db * 16 + l16) * LDV + t2 * 32 + lg * 4];
-          u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
-          u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
-          u32x4_t va = u32x4_t{lo.x, lo.y, hi.x, hi.y};
-          o[db][0] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[0][t2]), o[db][0]);
-          o[db][1] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[1][t2]), o[db][1]);
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = t0 + kb * 16 + lg * 4 + i;
+              float v = sacc[kb][rb][i] * a.scale_log2;
+              v = (key < nkeys && key <= qlim[rb]) ? v : NEG_INF;
+              sacc[kb][rb][i] = v;
+              mx = fmaxf(mx, v);
+            }
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const bool raise = mx > m_run[rb] + RESCALE_LOG2 || (m_run[rb] == NEG_INF && mx != NEG_INF);
+          const float m_new = raise ? mx : m_run[rb];
+          const float m_use = (m_new == NEG_INF) ? 0.f : m_new;
+          alpha[rb] = raise ? exp2f(m_run[rb] - m_use) : 1.0f;
+          need_any |= raise;
+          float sum = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float p = exp2f(sacc[kb][rb][i] - m_use);
+              sacc[kb][rb][i] = p;
+              sum += p;
+            }
+          sum += __shfl_xor(sum, 16, 64);
+          sum += __shfl_xor(sum, 32, 64);
+          l_run[rb] = l_run[rb] * alpha[rb] + sum;
+          m_run[rb] = m_new;
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) {
+            pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
+            pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
+            pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
+            pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
+          }
+        }
+        if (__ballot(need_any)) {
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            o[db][0] *= alpha[0];
+            o[db][1] *= alpha[1];
+          }
+        }
+
+        // O^T += V^T P^T; transposing LDS reads: lane i of a 16-lane group reads
+        // row K0 + i/4, dims 4 (i%4).. of a d-block and receives dim (block + i)
+        // of rows K0..K0+3.
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) {
+            s16x4_t part[2];
+#pragma unroll
+            for (int hlf = 0; hlf < 2; ++hlf) {
+              const unsigned char* p = sV + vbase[db & 3] + (t2 * 32 + hlf * 16) * S::ROW_BYTES + 128 * (db >> 2);
+              part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+            }
+            u32x4_t va;
+            __builtin_memcpy(&va, part, 16);
+            o[db][0] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[0][t2]), o[db][0]);
+            o[db][1] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[1][t2]), o[db][1]);
+          }
         }
       }
+      __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+      cur ^= 1;
     }
 
     // epilogue: normalise, write the partial (or the local window) and its LSE
@@ -266,6 +322,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     }
   }
 }
+
 
 // S6: per (query, KV head), one wave.  Seeds with the local window, then
 // folds the query's cluster partials in cluster order (query-major order of
@@ -326,7 +383,14 @@ __global__ __launch_bounds__(256) void combine_kernel(
 
 template <int D, int G>
 int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), 0, stream, a);
+  const size_t lds = AttnTileShape<D>::LDS_BYTES;
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)attn_items_kernel<D, G>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), lds, stream, a);
   return SBSA_OK;
 }
 
