@@ -135,13 +135,16 @@ int sbsa_reverse_index(const int32_t* qmask, int num_queries, int num_kv_heads, 
 /* ---- S5: KV-outer prefill attention ---------------------------------------------
  * The work list replacing the per-(cluster, KV head) FA3 varlen calls and the
  * local-window call of kv_outer_attention (semblo/vllm_plugin/kv_outer.py:661-753).
- * items are int4 {head, cluster or -1 (local window), first query slot, count};
- * queries_per_item = 128 / (Hq/Hkv). */
+ * items are int4 {head, cluster or -1 (local window), first query slot, count},
+ * grouped in one segment per XCD (the query tiles of a KV head's window, and
+ * those of one cluster, share an XCD and its L2); queue (int32[24]) receives
+ * the segments' sizes and offsets and zeroed counters.  queries_per_item =
+ * 128 / (Hq/Hkv). */
 int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
                                  int num_clusters, int queries_per_item);
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
                        int num_queries, int queries_per_item, int has_local, void* items,
-                       int64_t items_cap, int32_t* n_items, int32_t* counter, hipStream_t stream);
+                       int64_t items_cap, int32_t* queue, hipStream_t stream);
 
 /* Attention over the work list (kv_outer.py:482-816; dense chunks:
  * fused_prefill.py:155-189).  q [Qc, Hq, dim] (strides q_sq, q_sh); packed
@@ -159,7 +162,7 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
                         int64_t packed_len, const void* k_orig, const void* v_orig, int64_t o_st,
                         int64_t o_sh, const int32_t* indptr, const int32_t* nvis, int num_clusters,
                         const int32_t* rev_indptr, const int32_t* qvals, const void* items,
-                        const int32_t* n_items, int32_t* counter, void* part_o, float* part_lse,
+                        int32_t* queue, void* part_o, float* part_lse,
                         void* local_o, int64_t lo_sq, int64_t lo_sh, float* local_lse,
                         int64_t chunk_start, int64_t wstart, float sm_scale, int grid,
                         hipStream_t stream);

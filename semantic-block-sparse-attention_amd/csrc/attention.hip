@@ -33,8 +33,7 @@ struct AttnArgs {
   const int32_t* rev_indptr;// [Hkv*C + 1]
   const int32_t* qvals;     // [nnz] query slots per (head, cluster)
   const int4* items;
-  const int32_t* n_items;
-  int32_t* counter;
+  int32_t* queue;           // n[8], offset[8], counter[8]: one work queue per XCD
   bf16_t* part_o;           // [nnz, G, D]
   float* part_lse;          // [nnz, G]
   bf16_t* local_o;          // [Qc, Hq, D] strided
@@ -84,8 +83,11 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int total = *a.n_items;
   const float NEG_INF = -INFINITY;
+  // blocks are dispatched round-robin over the 8 XCDs: take work from this
+  // XCD's queue, then steal from the others
+  const int home = blockIdx.x & 7;
+  int probe = 0;
 
   // --- per-lane address bases (fixed for the kernel) ---------------------
   // loads: instruction m of this wave covers rows r0 + m * 4 * ROWS_PER_INST
@@ -105,12 +107,19 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   for (int dl = 0; dl < 4; ++dl)
     vbase[dl] = (lg * 4 + (l16 >> 2)) * S::ROW_BYTES + 32 * (dl ^ z) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
 
-  while (true) {
-    if (threadIdx.x == 0) s_item = atomicAdd(a.counter, 1);
+  while (probe < 8) {
+    const int x = (home + probe) & 7;
+    if (threadIdx.x == 0) {
+      const int v = atomicAdd(&a.queue[16 + x], 1);
+      s_item = v < a.queue[x] ? a.queue[8 + x] + v : -1;
+    }
     __syncthreads();
     const int idx = s_item;
     __syncthreads();
-    if (idx >= total) break;
+    if (idx < 0) {
+      ++probe;
+      continue;
+    }
     const int4 it = a.items[idx];
     const int h = it.x, c = it.y, qb = it.z, qn = it.w;
     const bool local = c < 0;
@@ -442,11 +451,11 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
                         int64_t packed_len, const void* k_orig, const void* v_orig, int64_t o_st,
                         int64_t o_sh, const int32_t* indptr, const int32_t* nvis, int num_clusters,
                         const int32_t* rev_indptr, const int32_t* qvals, const void* items,
-                        const int32_t* n_items, int32_t* counter, void* part_o, float* part_lse,
+                        int32_t* queue, void* part_o, float* part_lse,
                         void* local_o, int64_t lo_sq, int64_t lo_sh, float* local_lse,
                         int64_t chunk_start, int64_t wstart, float sm_scale, int grid,
                         hipStream_t stream) {
-  if (!q || !k_orig || !v_orig || !items || !n_items || !counter || !local_o) return SBSA_ERR_ARG;
+  if (!q || !k_orig || !v_orig || !items || !queue || !local_o) return SBSA_ERR_ARG;
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads) return SBSA_ERR_ARG;
   if (q_sq % 8 || q_sh % 8 || o_st % 8 || o_sh % 8 || lo_sq % 4 || lo_sh % 4) return SBSA_ERR_ARG;
   if (chunk_start < wstart || wstart < 0) return SBSA_ERR_ARG;
@@ -465,8 +474,7 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   a.rev_indptr = rev_indptr;
   a.qvals = qvals;
   a.items = (const int4*)items;
-  a.n_items = n_items;
-  a.counter = counter;
+  a.queue = queue;
   a.part_o = (bf16_t*)part_o;
   a.part_lse = part_lse;
   a.local_o = (bf16_t*)local_o;

@@ -272,50 +272,108 @@ __global__ __launch_bounds__(1024) void rev_scan_kernel(const int32_t* __restric
   }
 }
 
-// Work list of the KV-outer body: local-window items first (the longest, the
-// last query tiles, first), then one item per (head, cluster, query tile).
-// Item = {head, cluster or -1, first query slot, query count}.
+// Work list of the KV-outer body, one segment per XCD so that the items that
+// read the same K/V (the query tiles of one KV head's window, the query tiles
+// of one cluster) run on one XCD and share its L2.  Items within a segment:
+// local-window items first (longest first), then cluster items.  Item =
+// {head, cluster or -1, first query slot, query count}.  queue = {n[8],
+// off[8], counter[8]}; the counters are zeroed here.
+__device__ __forceinline__ int local_xcd(int h, int tile, int hkv) {
+  const int per = hkv >= 8 ? 1 : 8 / hkv;      // XCDs per KV head
+  return ((h * per) + (tile % per)) & 7;
+}
+__device__ __forceinline__ int cluster_xcd(int h, int c, int C) { return (h * C + c) & 7; }
+
 __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __restrict__ rev_counts,
                                                            int hkv, int C, int Qc, int QT,
                                                            int has_local, int4* __restrict__ items,
-                                                           int32_t* __restrict__ n_items,
-                                                           int32_t* __restrict__ counter,
+                                                           int32_t* __restrict__ queue,
                                                            int64_t cap) {
+  __shared__ int cnt[8];
+  __shared__ int off[8];
   __shared__ int wsum[16];
   __shared__ int carry;
   const int nloc = has_local ? (Qc + QT - 1) / QT : 0;
+  const int nl = nloc * hkv;
+  const int ncl = hkv * C;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int e = threadIdx.x; e < nloc * hkv; e += 1024) {
-    int k = e / hkv, h = e % hkv;
-    int tile = nloc - 1 - k;
-    int qb = tile * QT;
-    int qn = min(QT, Qc - qb);
-    if (e < cap) items[e] = make_int4(h, -1, qb, qn);
-  }
-  if (threadIdx.x == 0) carry = nloc * hkv;
+  if (threadIdx.x < 8) cnt[threadIdx.x] = 0;
   __syncthreads();
-  const int n = hkv * C;
-  for (int base = 0; base < n; base += 1024) {
-    int i = base + threadIdx.x;
-    int cnt = (i < n) ? rev_counts[i] : 0;
-    int k = (cnt + QT - 1) / QT;
-    int incl = wave_incl_scan(k);
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    int off = carry;
-    for (int w = 0; w < wave; ++w) off += wsum[w];
-    int first = off + incl - k;
-    for (int j = 0; j < k; ++j) {
-      int qb = j * QT;
-      if (first + j < cap) items[first + j] = make_int4(i / C, i % C, qb, min(QT, cnt - qb));
-    }
-    __syncthreads();
-    if (threadIdx.x == 1023) carry = off + incl;
-    __syncthreads();
+  for (int e = threadIdx.x; e < nl; e += 1024) {
+    const int k = e / hkv, h = e % hkv;
+    atomicAdd(&cnt[local_xcd(h, nloc - 1 - k, hkv)], 1);
   }
+  for (int e = threadIdx.x; e < ncl; e += 1024) {
+    const int n = (rev_counts[e] + QT - 1) / QT;
+    if (n) atomicAdd(&cnt[cluster_xcd(e / C, e % C, C)], n);
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    *n_items = (int32_t)min((int64_t)carry, cap);
-    *counter = 0;
+    int run = 0;
+    for (int x = 0; x < 8; ++x) {
+      off[x] = run;
+      run += cnt[x];
+    }
+  }
+  __syncthreads();
+  for (int x = 0; x < 8; ++x) {
+    if (threadIdx.x == 0) carry = off[x];
+    __syncthreads();
+    // local items of this XCD, in order
+    for (int base = 0; base < nl; base += 1024) {
+      const int e = base + threadIdx.x;
+      int k = 0, h = 0, tile = 0;
+      bool mine = false;
+      if (e < nl) {
+        k = e / hkv;
+        h = e % hkv;
+        tile = nloc - 1 - k;
+        mine = local_xcd(h, tile, hkv) == x;
+      }
+      const int f = mine ? 1 : 0;
+      const int incl = wave_incl_scan(f);
+      if (lane == 63) wsum[wave] = incl;
+      __syncthreads();
+      int o = carry;
+      for (int w = 0; w < wave; ++w) o += wsum[w];
+      if (mine) {
+        const int pos = o + incl - 1;
+        const int qb = tile * QT;
+        if (pos < cap) items[pos] = make_int4(h, -1, qb, min(QT, Qc - qb));
+      }
+      __syncthreads();
+      if (threadIdx.x == 1023) carry = o + incl;
+      __syncthreads();
+    }
+    // cluster items of this XCD, in (head, cluster) order
+    for (int base = 0; base < ncl; base += 1024) {
+      const int e = base + threadIdx.x;
+      int n = 0, cntq = 0;
+      if (e < ncl && cluster_xcd(e / C, e % C, C) == x) {
+        cntq = rev_counts[e];
+        n = (cntq + QT - 1) / QT;
+      }
+      const int incl = wave_incl_scan(n);
+      if (lane == 63) wsum[wave] = incl;
+      __syncthreads();
+      int o = carry;
+      for (int w = 0; w < wave; ++w) o += wsum[w];
+      const int first = o + incl - n;
+      for (int j = 0; j < n; ++j) {
+        const int qb = j * QT;
+        if (first + j < cap) items[first + j] = make_int4(e / C, e % C, qb, min(QT, cntq - qb));
+      }
+      __syncthreads();
+      if (threadIdx.x == 1023) carry = o + incl;
+      __syncthreads();
+    }
+  }
+  if (threadIdx.x < 8) {
+    const int x = threadIdx.x;
+    const int64_t end = min((int64_t)off[x] + cnt[x], cap);
+    queue[x] = (int32_t)max((int64_t)0, end - off[x]);   // n
+    queue[8 + x] = off[x];                               // offset
+    queue[16 + x] = 0;                                   // counter
   }
 }
 
@@ -434,11 +492,11 @@ int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
 
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
                        int num_queries, int queries_per_item, int has_local, void* items,
-                       int64_t items_cap, int32_t* n_items, int32_t* counter, hipStream_t stream) {
-  if (!rev_counts || !items || !n_items || !counter || queries_per_item < 1) return SBSA_ERR_ARG;
+                       int64_t items_cap, int32_t* queue, hipStream_t stream) {
+  if (!rev_counts || !items || !queue || queries_per_item < 1) return SBSA_ERR_ARG;
   hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), 0, stream, rev_counts, num_kv_heads,
-                     num_clusters, num_queries, queries_per_item, has_local, (int4*)items, n_items,
-                     counter, items_cap);
+                     num_clusters, num_queries, queries_per_item, has_local, (int4*)items, queue,
+                     items_cap);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }

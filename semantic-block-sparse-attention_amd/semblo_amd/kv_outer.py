@@ -31,7 +31,7 @@ def queries_per_item(q_per_kv: int) -> int:
 
 def default_grid(device: torch.device) -> int:
     props = torch.cuda.get_device_properties(device)
-    return int(props.multi_processor_count) * 2
+    return int(props.multi_processor_count)
 
 
 def build_reverse_index(qmask: torch.Tensor, live: torch.Tensor, *, num_queries: int,
@@ -104,17 +104,17 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
     qt = queries_per_item(g)
     bound = _lib.query("sbsa_prefill_items_bound", nnz, qn, hkv, c, qt)
     items = torch.empty(max(bound, 1), 4, dtype=torch.int32, device=dev)
-    n_items = torch.empty(2, dtype=torch.int32, device=dev)
+    queue = torch.empty(24, dtype=torch.int32, device=dev)
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(items), bound,
-              _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+              _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               _lib.ptr(packed_kv), packed_kv.shape[1], _lib.ptr(k_loc), _lib.ptr(v_loc),
               k_loc.stride(0), k_loc.stride(1), _lib.ptr(bucket_indptr), _lib.ptr(nvis), c,
-              _lib.ptr(rev_indptr), _lib.ptr(qvals), _lib.ptr(items), _lib.ptr(n_items),
-              _lib.ptr(n_items[1:]), _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
+              _lib.ptr(rev_indptr), _lib.ptr(qvals), _lib.ptr(items), _lib.ptr(queue),
+              _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
               local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), int(chunk_start),
               int(wstart), float(sm_scale), int(grid or default_grid(dev)), s)
     if timing is not None:
@@ -148,17 +148,17 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
     bound = hkv * ((qn + qt - 1) // qt) + 1
     items = torch.empty(bound, 4, dtype=torch.int32, device=dev)
-    n_items = torch.empty(2, dtype=torch.int32, device=dev)
+    queue = torch.empty(24, dtype=torch.int32, device=dev)
     if out is None:
         out = torch.empty_like(q)
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(items),
-              bound, _lib.ptr(n_items), _lib.ptr(n_items[1:]), s)
+              bound, _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               None, 0, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), None, None, 32, None,
-              None, _lib.ptr(items), _lib.ptr(n_items), _lib.ptr(n_items[1:]), None, None,
+              None, _lib.ptr(items), _lib.ptr(queue), None, None,
               _lib.ptr(out), out.stride(0), out.stride(1), None, int(chunk_start), 0,
               float(sm_scale), int(grid or default_grid(dev)), s)
     if timing is not None:
