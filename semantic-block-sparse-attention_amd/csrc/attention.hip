@@ -175,17 +175,21 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       const bool ok = i < qn;
       int qidx = 0;
       if (ok) qidx = local ? qb + i : a.qvals[entry0 + i];
-      qidx_r[rb] = qidx;
+      qidx_r[rb] = ok ? qidx : -1;
       qlim[rb] = local ? (int)(a.chunk_start + qidx - a.wstart) : 0x7fffffff;
       const bf16_t* src = a.q + (int64_t)qidx * a.q_sq + (int64_t)(h * G + j) * a.q_sh + lg * 8;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
         qr[rb][s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
     }
-    // the last key any row of this wave may see
+    // the last key any row of this wave may see, and the last key every row sees
     int wave_lim = max(qlim[0], qlim[1]);
+    int wave_min = min(qidx_r[0] >= 0 ? qlim[0] : 0x7fffffff, qidx_r[1] >= 0 ? qlim[1] : 0x7fffffff);
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
+    for (int o = 1; o < 64; o <<= 1) {
+      wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
+      wave_min = min(wave_min, __shfl_xor(wave_min, o, 64));
+    }
 
     f32x4_t o[DB][2];
 #pragma unroll
@@ -224,7 +228,19 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           }
         }
 
-        // online softmax in the log2 domain, with a lazily raised maximum
+        // online softmax in the log2 domain, with a lazily raised maximum;
+        // only tiles that cross the item's end or a row's causal limit are masked
+        if (t0 + KT > nkeys || t0 + KT - 1 > wave_min) {
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int key = t0 + kb * 16 + lg * 4 + i;
+                if (!(key < nkeys && key <= qlim[rb])) sacc[kb][rb][i] = NEG_INF;
+              }
+        }
         u32x4_t pb[2][2];
         float alpha[2];
         bool need_any = false;
@@ -234,15 +250,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
 #pragma unroll
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = t0 + kb * 16 + lg * 4 + i;
-              float v = sacc[kb][rb][i] * a.scale_log2;
-              v = (key < nkeys && key <= qlim[rb]) ? v : NEG_INF;
-              sacc[kb][rb][i] = v;
-              mx = fmaxf(mx, v);
-            }
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kb][rb][i]);
           mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
           mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          mx *= a.scale_log2;                      // scale > 0: the maximum commutes
           const bool raise = mx > m_run[rb] + RESCALE_LOG2 || (m_run[rb] == NEG_INF && mx != NEG_INF);
           const float m_new = raise ? mx : m_run[rb];
           const float m_use = (m_new == NEG_INF) ? 0.f : m_new;
@@ -253,7 +264,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              float p = exp2f(sacc[kb][rb][i] - m_use);
+              float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rb][i], a.scale_log2, -m_use));
               sacc[kb][rb][i] = p;
               sum += p;
             }
@@ -307,7 +318,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     for (int rb = 0; rb < 2; ++rb) {
       const int R = wave * 32 + rb * 16 + l16;
       const int i = R / G, j = R % G;
-      if (i >= qn) continue;
+      if (qidx_r[rb] < 0) continue;
       const float l = l_run[rb];
       const float inv = (l > 0.f) ? 1.0f / l : 0.f;
       const float lse = (l > 0.f) ? (m_run[rb] + log2f(l)) * 0.69314718055994531f : NEG_INF;

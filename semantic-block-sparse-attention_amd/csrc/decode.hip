@@ -59,6 +59,7 @@ struct DecodeArgs {
 };
 
 constexpr int MAX_C = 1024;
+constexpr int MAX_SPLITS = 512;   // prompt + suffix splits of one step
 
 // ---------------------------------------------------------------- select ---
 template <int D>
@@ -261,7 +262,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   __shared__ float s_m[4][G];
   __shared__ float s_l[4][G];
   __shared__ float s_acc[4][G][D];
-  __shared__ float s_scale[G][64];
+  __shared__ float s_scale[G][MAX_SPLITS];
   __shared__ int s_last;
   const int h = blockIdx.x;
   const int split = blockIdx.y;
@@ -450,37 +451,43 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   __threadfence();
   float* m_sh = &s_m[0][0];
   float* den_sh = &s_l[0][0];
-  if (threadIdx.x < G) {
-    const int j = threadIdx.x;
+  // split scales: wave w takes heads w, w+4, ..; its lanes stride the splits
+  for (int j = wave; j < G; j += 4) {
     const int hq = h * G + j;
+    const float* pm = a.pm + (int64_t)hq * S;
+    const float* pl = a.pl + (int64_t)hq * S;
     float mx = -INFINITY;
-    for (int s = 0; s < S; ++s) mx = fmaxf(mx, __builtin_nontemporal_load(&a.pm[(int64_t)hq * S + s]));
+    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, __builtin_nontemporal_load(pm + s));
+    mx = wave_max(mx);
     const float mu = (mx == -INFINITY) ? 0.f : mx;
     float den = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float pmv = __builtin_nontemporal_load(&a.pm[(int64_t)hq * S + s]);
+    for (int s = lane; s < S; s += 64) {
+      const float pmv = __builtin_nontemporal_load(pm + s);
       const float sc = (pmv == -INFINITY) ? 0.f : exp2f(pmv - mu);
-      if (s < 64) s_scale[j][s] = sc;
-      den += __builtin_nontemporal_load(&a.pl[(int64_t)hq * S + s]) * sc;
+      s_scale[j][s] = sc;
+      den += __builtin_nontemporal_load(pl + s) * sc;
     }
-    m_sh[j] = mu;
-    den_sh[j] = den;
+    den = wave_sum(den);
+    if (lane == 0) {
+      m_sh[j] = mu;
+      den_sh[j] = den;
+    }
   }
   __syncthreads();
   for (int e = threadIdx.x; e < G * D; e += 256) {
     const int j = e / D, d = e % D;
     const int hq = h * G + j;
-    float num = 0.f;
-    for (int s = 0; s < S; ++s) {
-      float sc;
-      if (s < 64) {
-        sc = s_scale[j][s];
-      } else {
-        const float pmv = __builtin_nontemporal_load(&a.pm[(int64_t)hq * S + s]);
-        sc = (pmv == -INFINITY) ? 0.f : exp2f(pmv - m_sh[j]);
-      }
-      num += __builtin_nontemporal_load(&a.pacc[((int64_t)hq * S + s) * D + d]) * sc;
+    const float* src = a.pacc + (int64_t)hq * S * D + d;
+    float num0 = 0.f, num1 = 0.f, num2 = 0.f, num3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= S; s += 4) {
+      num0 += __builtin_nontemporal_load(src + (int64_t)s * D) * s_scale[j][s];
+      num1 += __builtin_nontemporal_load(src + (int64_t)(s + 1) * D) * s_scale[j][s + 1];
+      num2 += __builtin_nontemporal_load(src + (int64_t)(s + 2) * D) * s_scale[j][s + 2];
+      num3 += __builtin_nontemporal_load(src + (int64_t)(s + 3) * D) * s_scale[j][s + 3];
     }
+    for (; s < S; ++s) num0 += __builtin_nontemporal_load(src + (int64_t)s * D) * s_scale[j][s];
+    const float num = (num0 + num1) + (num2 + num3);
     const float den = den_sh[j];
     a.out[(int64_t)hq * a.out_sh + d] = f2bf(den == 0.f ? 0.f : num / den);
     if (d == 0 && a.out_lse)
@@ -540,7 +547,7 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   const int G = num_q_heads / num_kv_heads;
   const int C = num_clusters;
   if (C % 64 || C > MAX_C) return SBSA_ERR_UNSUPPORTED;
-  if (num_splits + suffix_splits > 4096) return SBSA_ERR_UNSUPPORTED;
+  if (num_splits + suffix_splits > MAX_SPLITS) return SBSA_ERR_UNSUPPORTED;
   if ((packed_len + 1) * num_kv_heads * (int64_t)dim >= (1ll << 31) ||
       (suffix_nblk * suffix_block + 1) * num_kv_heads * (int64_t)dim >= (1ll << 31))
     return SBSA_ERR_UNSUPPORTED;

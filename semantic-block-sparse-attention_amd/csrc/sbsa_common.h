@@ -1,7 +1,7 @@
 // Shared device helpers for the gfx950 kernels of libsbsa.
 //
 // bf16 values are carried as raw uint16_t bit patterns; conversions are
-// explicit (round to nearest even, as torch's .to(torch.bfloat16)).  MFMA
+// explicit (round to nearest even, as torch's .to(torch.bfloat16), in hardware).  MFMA
 // operands use clang's __bf16 vector types.
 #pragma once
 
@@ -20,18 +20,25 @@ typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
+// gfx950 converts with v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN.
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (bf16_t)((u >> 16) | 0x40u);
-  uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(r >> 16);
+  __bf16 b = (__bf16)f;
+  bf16_t r;
+  __builtin_memcpy(&r, &b, 2);
+  return r;
 }
 
 // fp32 -> bf16 -> fp32 (the value a bf16 tensor would hold).
 __device__ __forceinline__ float round_bf16(float f) { return bf2f(f2bf(f)); }
 
 __device__ __forceinline__ uint32_t pack2bf(float a, float b) {
-  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  bf16x2_t v = __builtin_convertvector(f32x2_t{a, b}, bf16x2_t);
+  uint32_t r;
+  __builtin_memcpy(&r, &v, 4);
+  return r;
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
