@@ -8,15 +8,20 @@
 //                             suffix splits via the block table)
 //   fused_decode.py:334-358   _decode_merge_kernel
 //
-// Two launches, no host reads, no allocation: every size the kernels need
+// Three launches, no host reads, no allocation: every size the kernels need
 // (the position, the selected token count) is read on the device, so a HIP
 // graph can capture the step and replay it at fixed addresses.
-//   1. select: one block per KV head -- suffix write, routing, scores on MFMA,
-//      per-component LSE, bisection under the budget, CSR of the selection.
-//   2. attend: one 4-wave block per (KV head, split) over the CSR's token
-//      range (or a range of suffix tiles); the waves' partials are combined
-//      in LDS, and the last block of a head to finish merges every split of
-//      the head into the output (a per-head counter, reset by that block).
+//   1. select: one block per KV head -- routing, scores on MFMA, per-component
+//      LSE, bisection under the budget and the CSR of the selection (wave 0),
+//      while the other waves write the token's K/V into the suffix store.
+//   2. attend: one block per (KV head, split).  A head's keys are one list,
+//      the selected prompt rows (in CSR order) followed by the live suffix
+//      rows; each split takes an even, 32-aligned range of it.  The block
+//      resolves its rows' addresses into LDS, each wave gathers 32-key tiles
+//      straight into LDS (global loads to LDS) and runs S^T = K Q^T and
+//      O^T = V^T P^T on MFMA with the G query heads as columns; the waves'
+//      partials are folded in LDS into the split's partial.
+//   3. merge: one block per (query head, 64 dimensions) folds the splits.
 #include "sbsa_common.h"
 
 namespace {
@@ -46,7 +51,6 @@ struct DecodeArgs {
   int32_t* rcum;
   int32_t* rcount;          // [Hkv]
   int32_t* rtokens;
-  int32_t* done;            // [Hkv] finished-split counters (zero between steps)
   float* pacc;              // [Hq, S, D]
   float* pm;                // [Hq, S]
   float* pl;
@@ -84,22 +88,21 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       ip[k] = (k < nk) ? a.indptr[h * (C + 1) + lane + 64 * k] : 0;
     }
   }
-  // 0. suffix write of this KV head (a position past the reservation is not
-  //    written: the table does not cover it)
-  if (a.k_new) {
-    const int64_t p = *a.pos;
-    if (p >= a.prompt_len && p - a.prompt_len < (int64_t)a.max_tiles * 16) {
-      const int64_t blk = p / a.BS;
-      const int64_t off = p - blk * a.BS;
-      const int64_t phys = a.table[blk];
-      const int64_t plane = a.suffix_nblk * a.BS * a.Hkv * D;
-      bf16_t* dst = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
-      for (int d = threadIdx.x; d < D; d += 256) {
-        dst[d] = a.k_new[(int64_t)h * a.kn_sh + d];
-        dst[plane + d] = a.v_new[(int64_t)h * a.kn_sh + d];
-      }
+  const int64_t q_pos = *a.pos;   // used by the suffix write at the end
+  // the first two codebook tiles of this wave, in flight during the routing
+  const bf16_t* cb = a.codebooks + (int64_t)h * 2 * C * half;
+  auto load_cb = [&](int cbk, u32x4_t* b) {
+    const int cc = cbk * 16 + (lane & 15);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      int d = s * 32 + (lane >> 4) * 8;
+      int part = d / half;
+      b[s] = *reinterpret_cast<const u32x4_t*>(cb + ((int64_t)part * C + cc) * half + (d - part * half));
     }
-  }
+  };
+  u32x4_t b0[KS], b1[KS];
+  if (wave < C / 16) load_cb(wave, b0);
+  if (wave + 4 < C / 16) load_cb(wave + 4, b1);
   // 1. routing vectors of the G query heads (rows >= G are zero)
   for (int e = threadIdx.x; e < 16 * (D / 8); e += 256) {
     int r = e / (D / 8), ch = e % (D / 8);
@@ -117,14 +120,14 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       ss += v[i] * v[i];
     }
     if (a.router_pass) {
-      float n1 = fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
+      float n1 = fmaxf(sqrtf(wave_sum_dpp(ss)), 1e-12f);
       float ss2 = 0.f;
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         v[i] = round_bf16(v[i] / n1);
         ss2 += v[i] * v[i];
       }
-      float n2 = fmaxf(sqrtf(wave_sum(ss2)), 1e-12f);
+      float n2 = fmaxf(sqrtf(wave_sum_dpp(ss2)), 1e-12f);
 #pragma unroll
       for (int i = 0; i < PER; ++i) v[i] = v[i] / n2;
     }
@@ -140,16 +143,8 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
 #pragma unroll
   for (int s = 0; s < KS; ++s)
     aop[s] = *reinterpret_cast<const u32x4_t*>(&svec[(lane & 15) * LDQ + s * 32 + (lane >> 4) * 8]);
-  const bf16_t* cb = a.codebooks + (int64_t)h * 2 * C * half;
-  for (int cbk = wave; cbk < C / 16; cbk += 4) {
+  auto score_tile = [&](int cbk, const u32x4_t* b) {
     const int cc = cbk * 16 + (lane & 15);
-    u32x4_t b[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      int d = s * 32 + (lane >> 4) * 8;
-      int part = d / half;
-      b[s] = *reinterpret_cast<const u32x4_t*>(cb + ((int64_t)part * C + cc) * half + (d - part * half));
-    }
     f32x4_t acc = f32x4_t{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < KS; ++s) acc = mfma16x16x32(as_bf16x8(aop[s]), as_bf16x8(b[s]), acc);
@@ -158,6 +153,13 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       int t = (lane >> 4) * 4 + i;
       if (t < G) ssc[t * C + cc] = acc[i] * a.inv_temp;
     }
+  };
+  if (wave < C / 16) score_tile(wave, b0);
+  if (wave + 4 < C / 16) score_tile(wave + 4, b1);
+  for (int cbk = wave + 8; cbk < C / 16; cbk += 4) {
+    u32x4_t b[KS];
+    load_cb(cbk, b);
+    score_tile(cbk, b);
   }
   __syncthreads();
   // 3. per component LSE, then w = exp(s - lse) in place
@@ -165,15 +167,30 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
     float* row = ssc + t * C;
     float m = -INFINITY;
     for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     float l = 0.f;
     for (int c = lane; c < C; c += 64) l += expf(row[c] - m);
-    l = wave_sum(l);
+    l = wave_sum_dpp(l);
     float lse = m + logf(l);
     for (int c = lane; c < C; c += 64) row[c] = expf(row[c] - lse);
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) {
+    // the token's K/V into the suffix store (a position past the reservation
+    // is not written: the table does not cover it)
+    if (a.k_new && q_pos >= a.prompt_len && q_pos - a.prompt_len < (int64_t)a.max_tiles * 16) {
+      const int64_t blk = q_pos / a.BS;
+      const int64_t off = q_pos - blk * a.BS;
+      const int64_t phys = a.table[blk];
+      const int64_t plane = a.suffix_nblk * a.BS * a.Hkv * D;
+      bf16_t* dst = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
+      for (int d = threadIdx.x - 64; d < D; d += 192) {
+        dst[d] = a.k_new[(int64_t)h * a.kn_sh + d];
+        dst[plane + d] = a.v_new[(int64_t)h * a.kn_sh + d];
+      }
+    }
+    return;
+  }
   // 4. bisection and CSR emission (wave 0); sizes are integers below 2^24, so
   //    the reference's fp32 sums are exact and equal these integer sums
   const float NEG = -3.4e38f, POS = 3.4e38f;
@@ -201,10 +218,10 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       live_total += live ? s : 0;
     }
   }
-  hi = wave_max(hi) + 1e-6f;
-  lo = wave_min(lo) - 1e-6f;
+  hi = wave_max_dpp(hi) + 1e-6f;
+  lo = wave_min_dpp(lo) - 1e-6f;
   lo = fminf(lo, hi - 1e-5f);
-  live_total = wave_sum_i32(live_total);
+  live_total = wave_sum_i32_dpp(live_total);
   const float budget = (a.sink > 0) ? fmaxf(a.target - (float)a.sink, 0.f) : a.target;
   const bool all_fit = (float)live_total < budget;
   for (int it = 0; it < a.iters; ++it) {
@@ -213,7 +230,7 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < 16; ++k)
       if (k < nk && score[k] >= mid) above += size[k];
-    above = wave_sum_i32(above);
+    above = wave_sum_i32_dpp(above);
     const bool reach = (float)above >= budget;
     lo = reach ? mid : lo;
     hi = reach ? hi : mid;
@@ -227,16 +244,16 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       const bool sel = (size[k] > 0 && score[k] >= theta) || (a.sink > 0 && c == 0 && sz[k] > 0);
       const int si = sel ? 1 : 0;
       const int sl = sel ? sz[k] : 0;
-      const int pi = wave_incl_scan(si);
-      const int pt = wave_incl_scan(sl);
+      const int pi = wave_incl_scan_dpp(si);
+      const int pt = wave_incl_scan_dpp(sl);
       if (sel) {
         const int p = carry_n + pi - 1;
         a.rstart[h * C + p] = ip[k];
         a.rlen[h * C + p] = sl;
         a.rcum[h * C + p] = carry_tok + pt - sl;
       }
-      carry_n += __shfl(pi, 63, 64);
-      carry_tok += __shfl(pt, 63, 64);
+      carry_n += __builtin_amdgcn_readlane(pi, 63);
+      carry_tok += __builtin_amdgcn_readlane(pt, 63);
     }
   }
   if (lane == 0) {
@@ -245,185 +262,212 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
   }
 }
 
-// ------------------------------------------------------------ attend+merge --
-// A 16-key tile: S = Q K^T on MFMA with the G query heads as rows (padded to
-// 16): lane (l16, lg) holds heads lg*4..lg*4+3 for key l16, and the softmax
-// runs in that layout.  P V runs on the vector units, each lane owning D/64
-// output dimensions of every head, with the probabilities and the V row
-// addresses broadcast by readlane.  The next tile's K and V are loaded before
-// the current one is consumed.
+// ---------------------------------------------------------------- attend ---
+constexpr int DT = 32;          // keys per wave tile
+constexpr int ROW_CHUNK = 256;  // rows whose addresses a block resolves at once
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// Per-wave LDS tile: DT rows of K then DT rows of V, each row D bf16 with
+// its 16-byte chunks permuted (K: chunk ^ (row % 8), V: chunk ^ 2 (row % 4))
+// so that the MFMA operand reads spread over the banks.
+template <int D>
+struct DecodeTile {
+  static constexpr int ROW_BYTES = 2 * D;
+  static constexpr int CH = D / 8;               // 16-byte chunks per row
+  static constexpr int RPI = 64 / CH;            // rows per wave load instruction
+  static constexpr int INSTS = DT / RPI;         // load instructions per K (or V) tile
+  static constexpr int KV_BYTES = DT * ROW_BYTES;
+  static constexpr int WAVE_BYTES = 2 * KV_BYTES;
+  static constexpr size_t LDS_BYTES = 4 * (size_t)WAVE_BYTES;
+};
+
 template <int D, int G>
 __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
+  using T = DecodeTile<D>;
   constexpr int KS = D / 32;
-  constexpr int DPL = D / 64;               // output dims per lane
-  constexpr int VW = DPL / 2;               // 32-bit words of V per lane and key
+  constexpr int DB = D / 16;
+  static_assert(G <= 16, "query heads per KV head");
+  static_assert(16 * G * D <= (int)T::LDS_BYTES, "wave partials fit the tile space");
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_dec[];
   __shared__ int s_rcum[MAX_C];
   __shared__ int s_rstart[MAX_C];
-  __shared__ float s_m[4][G];
-  __shared__ float s_l[4][G];
-  __shared__ float s_acc[4][G][D];
-  __shared__ float s_scale[G][MAX_SPLITS];
-  __shared__ int s_last;
+  __shared__ const bf16_t* s_kaddr[ROW_CHUNK];
+  __shared__ const bf16_t* s_vaddr[ROW_CHUNK];
+  __shared__ float s_m[4][16];
+  __shared__ float s_l[4][16];
   const int h = blockIdx.x;
   const int split = blockIdx.y;
-  const int S = a.nsplit + a.ssplit;
+  const int S = gridDim.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
+
+  // this split's range of the head's key list (prompt rows, then suffix rows)
   const int64_t q_pos = *a.pos;
-  const bool prompt = split < a.nsplit;
-
-  int count = 0, rcount = 0, t_lo = 0, t_hi = 0;
-  if (prompt) {
-    count = a.rtokens[h];
-    rcount = a.rcount[h];
-    for (int i = threadIdx.x; i < rcount; i += 256) {
-      s_rcum[i] = a.rcum[h * a.C + i];
-      s_rstart[i] = a.rstart[h * a.C + i];
-    }
-    const int ntiles = (count + 15) / 16;
-    const int per = (ntiles + a.nsplit - 1) / a.nsplit;
-    t_lo = split * per;
-    t_hi = min(t_lo + per, ntiles);
-  } else {
-    const int s = split - a.nsplit;
-    int64_t live64 = (q_pos - a.prompt_len) / 16 + 1;
-    live64 = live64 < 1 ? 1 : (live64 > a.max_tiles ? a.max_tiles : live64);
-    const int live = (int)live64;
-    const int per = (live + a.ssplit - 1) / a.ssplit;
-    t_lo = s * per;
-    t_hi = min(t_lo + per, live);
+  const int count = a.rtokens[h];
+  const int rcount = a.rcount[h];
+  int64_t nsuf64 = q_pos - a.prompt_len + 1;
+  nsuf64 = nsuf64 < 0 ? 0 : (nsuf64 > (int64_t)a.max_tiles * 16 ? (int64_t)a.max_tiles * 16 : nsuf64);
+  const int total = count + (int)nsuf64;
+  const int per = ((total + S - 1) / S + DT - 1) / DT * DT;
+  const int r_lo = min(split * per, total);
+  const int r_hi = min(r_lo + per, total);
+  for (int i = threadIdx.x; i < rcount; i += 256) {
+    s_rcum[i] = a.rcum[h * a.C + i];
+    s_rstart[i] = a.rstart[h * a.C + i];
   }
-  __syncthreads();
+  const int64_t pplane = a.packed_len * a.Hkv * D;
+  const int64_t splane = a.suffix_nblk * a.BS * a.Hkv * D;
 
-  const bf16_t* base = prompt ? a.packed : a.suffix_kv;
-  const int64_t vplane = prompt ? a.packed_len * a.Hkv * D : a.suffix_nblk * a.BS * a.Hkv * D;
-  // element offset of key l16 of tile t (its K row), or -1
-  auto key_elem = [&](int t) -> int {
-    if (prompt) {
-      const int o = t * 16 + l16;
-      if (o >= count) return -1;
-      int lo = 0, hi = rcount;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (s_rcum[mid] <= o) lo = mid + 1;
-        else hi = mid;
-      }
-      const int r = lo > 0 ? lo - 1 : 0;
-      const int row = s_rstart[r] + (o - s_rcum[r]);
-      return (row * a.Hkv + h) * D;
-    }
-    const int64_t p = a.prompt_len + (int64_t)t * 16 + l16;
-    if (p > q_pos) return -1;
-    const int64_t blk = p / a.BS;
-    const int64_t off = p - blk * a.BS;
-    const int64_t phys = a.table[blk];
-    return (int)(((phys * a.BS + off) * a.Hkv + h) * D);
-  };
-
-  u32x4_t qa[KS];
+  // Q^T as the B operand: column l16 is query head h*G + l16 (zero past G)
+  u32x4_t qr[KS];
   {
     const bool ok = l16 < G;
     const bf16_t* src = a.q_post + (int64_t)(h * G + (ok ? l16 : 0)) * a.q_sh + lg * 8;
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      qa[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
+      qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
   }
-  float m_run[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};   // heads lg*4 + i
-  float l_run[4] = {0.f, 0.f, 0.f, 0.f};
-  float acc[G][DPL];
-#pragma unroll
-  for (int j = 0; j < G; ++j)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[j][e] = 0.f;
 
-  u32x4_t kb[KS];
-  uint32_t vreg[16][VW];
-  int elem = -1;
-  auto load_tile = [&](int t) {
-    elem = key_elem(t);
+  // fixed per-lane LDS offsets
+  const int cpos = lane % T::CH;
+  const int xb = (l16 >> 2) & 1, xl = l16 & 3;
+  const int kbase_even = l16 * T::ROW_BYTES + 64 * xb + 16 * (lg ^ xl);
+  const int kbase_odd = l16 * T::ROW_BYTES - 64 * xb + 16 * (lg ^ xl);
+  const int z = (l16 >> 2) & 3;
+  int vbase[4];
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      kb[s] = elem >= 0 ? *reinterpret_cast<const u32x4_t*>(base + elem + s * 32 + lg * 8) : u32x4_t{0, 0, 0, 0};
-#pragma unroll
-    for (int n = 0; n < 16; ++n) {
-      const int rn = __builtin_amdgcn_readlane(elem, n);
-      const bf16_t* src = base + vplane + rn + lane * DPL;
-      if constexpr (VW == 2) {
-        u32x2_t w = rn >= 0 ? *reinterpret_cast<const u32x2_t*>(src) : u32x2_t{0, 0};
-        vreg[n][0] = w.x;
-        vreg[n][1] = w.y;
-      } else {
-        vreg[n][0] = rn >= 0 ? *reinterpret_cast<const uint32_t*>(src) : 0u;
-      }
-    }
-  };
+  for (int dl = 0; dl < 4; ++dl)
+    vbase[dl] = (lg * 4 + (l16 >> 2)) * T::ROW_BYTES + 32 * (dl ^ z) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
+  unsigned char* sK = smem_dec + wave * T::WAVE_BYTES;
+  unsigned char* sV = sK + T::KV_BYTES;
 
-  int t = t_lo + wave;
-  if (t < t_hi) load_tile(t);
-  for (; t < t_hi; t += 4) {
-    // S tile of the loaded keys
-    f32x4_t sacc = f32x4_t{0, 0, 0, 0};
+  float m_run = -INFINITY, l_run = 0.f;          // of query head l16
+  f32x4_t o[DB];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) sacc = mfma16x16x32(as_bf16x8(qa[s]), as_bf16x8(kb[s]), sacc);
-    const bool kvalid = elem >= 0;
-    uint32_t vcur[16][VW];
-#pragma unroll
-    for (int n = 0; n < 16; ++n)
-#pragma unroll
-      for (int w = 0; w < VW; ++w) vcur[n][w] = vreg[n][w];
-    if (t + 4 < t_hi) load_tile(t + 4);        // next tile in flight
-    // softmax bookkeeping for this lane's heads (lg*4 + i), over the 16 keys
-    float alpha[4], p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = kvalid ? sacc[i] * a.scale_log2 : -INFINITY;
-      float mx = v;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-      const float m_new = fmaxf(m_run[i], mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      alpha[i] = exp2f(m_run[i] - m_use);
-      p[i] = exp2f(v - m_use);
-      float sum = p[i];
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
-      l_run[i] = l_run[i] * alpha[i] + sum;
-      m_run[i] = m_new;
-    }
-    // P V: every lane, every head, its own dims
-#pragma unroll
-    for (int j = 0; j < G; ++j) {
-      const float al = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha[j & 3]), (j >> 2) * 16));
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) acc[j][e] *= al;
-#pragma unroll
-      for (int n = 0; n < 16; ++n) {
-        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[j & 3]), (j >> 2) * 16 + n));
-#pragma unroll
-        for (int w = 0; w < VW; ++w) {
-          acc[j][2 * w] += pj * __uint_as_float(vcur[n][w] << 16);
-          acc[j][2 * w + 1] += pj * __uint_as_float(vcur[n][w] & 0xffff0000u);
+  for (int db = 0; db < DB; ++db) o[db] = f32x4_t{0, 0, 0, 0};
+  __syncthreads();
+
+  for (int c0 = r_lo; c0 < r_hi; c0 += ROW_CHUNK) {
+    const int cn = min(ROW_CHUNK, r_hi - c0);
+    {
+      // address of row c0 + tid of the key list (rows past cn: a valid dummy row)
+      const int oo = c0 + (int)threadIdx.x;
+      const bf16_t* kp = a.packed + (int64_t)h * D;
+      int64_t vo = pplane;
+      if ((int)threadIdx.x < cn) {
+        if (oo < count) {
+          int lo = 0, hi = rcount;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (s_rcum[mid] <= oo) lo = mid + 1;
+            else hi = mid;
+          }
+          const int r = lo > 0 ? lo - 1 : 0;
+          const int64_t row = (int64_t)s_rstart[r] + (oo - s_rcum[r]);
+          kp = a.packed + (row * a.Hkv + h) * D;
+        } else {
+          const int64_t p = a.prompt_len + (oo - count);
+          const int64_t blk = p / a.BS;
+          const int64_t off = p - blk * a.BS;
+          const int64_t phys = a.table[blk];
+          kp = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
+          vo = splane;
         }
       }
+      s_kaddr[threadIdx.x] = kp;
+      s_vaddr[threadIdx.x] = kp + vo;
     }
-  }
-  // the wave's partial -> LDS
-  if (l16 == 0) {
+    __syncthreads();
+    for (int t0 = wave * DT; t0 < cn; t0 += 4 * DT) {
+      // gather the tile's K and V rows into this wave's LDS tile
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = lg * 4 + i;
-      if (j < G) {
-        s_m[wave][j] = m_run[i];
-        s_l[wave][j] = l_run[i];
+      for (int m = 0; m < T::INSTS; ++m) {
+        const int r = m * T::RPI + lane / T::CH;
+        const bf16_t* kr = s_kaddr[t0 + r];
+        const bf16_t* vr = s_vaddr[t0 + r];
+        __builtin_amdgcn_global_load_lds((const void*)(kr + 8 * (cpos ^ (r & 7))),
+                                         (lds_void_t*)(sK + m * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(vr + 8 * (cpos ^ ((r & 3) << 1))),
+                                         (lds_void_t*)(sV + m * 1024), 16, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of query head l16
+      f32x4_t sacc[2] = {f32x4_t{0, 0, 0, 0}, f32x4_t{0, 0, 0, 0}};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const unsigned char* kb0 = sK + ((s & 1) ? kbase_odd : kbase_even) + 64 * s;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * T::ROW_BYTES);
+          sacc[kb] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[s]), sacc[kb]);
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (t0 + kb * 16 + lg * 4 + i >= cn) sacc[kb][i] = -INFINITY;
+          mx = fmaxf(mx, sacc[kb][i]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx *= a.scale_log2;
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][i], a.scale_log2, -m_use));
+          sacc[kb][i] = p;
+          sum += p;
+        }
+      sum += __shfl_xor(sum, 16, 64);
+      sum += __shfl_xor(sum, 32, 64);
+      l_run = l_run * alpha + sum;
+      m_run = m_new;
+      // P^T as the B operand: keys {4 lg..4 lg+3, 16+4 lg..16+4 lg+3} of head l16
+      u32x4_t pb;
+      pb.x = pack2bf(sacc[0][0], sacc[0][1]);
+      pb.y = pack2bf(sacc[0][2], sacc[0][3]);
+      pb.z = pack2bf(sacc[1][0], sacc[1][1]);
+      pb.w = pack2bf(sacc[1][2], sacc[1][3]);
+      // O^T = alpha O^T + V^T P^T (V^T by transposing LDS reads in the same key order)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        s16x4_t part[2];
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf) {
+          const unsigned char* p = sV + vbase[db & 3] + hlf * 16 * T::ROW_BYTES + 128 * (db >> 2);
+          part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+        }
+        u32x4_t va;
+        __builtin_memcpy(&va, part, 16);
+        o[db] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb), o[db] * alpha);
       }
     }
+    __syncthreads();
   }
+
+  // fold the four waves into the split's partial (tile space reused)
+  float* s_acc = reinterpret_cast<float*>(smem_dec);   // [4][G][D]
+  if (l16 < G) {
+    if (lg == 0) {
+      s_m[wave][l16] = m_run;
+      s_l[wave][l16] = l_run;
+    }
 #pragma unroll
-  for (int j = 0; j < G; ++j)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) s_acc[wave][j][lane * DPL + e] = acc[j][e];
+      for (int i = 0; i < 4; ++i) s_acc[(wave * G + l16) * D + db * 16 + lg * 4 + i] = o[db][i];
+  }
   __syncthreads();
-  // combine the four waves into this split's partial
   for (int e = threadIdx.x; e < G * D; e += 256) {
     const int j = e / D, d = e % D;
     const float mx = fmaxf(fmaxf(s_m[0][j], s_m[1][j]), fmaxf(s_m[2][j], s_m[3][j]));
@@ -432,7 +476,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const float sc = (s_m[w][j] == -INFINITY) ? 0.f : exp2f(s_m[w][j] - mu);
-      num += s_acc[w][j][d] * sc;
+      num += s_acc[(w * G + j) * D + d] * sc;
       den += s_l[w][j] * sc;
     }
     const int hq = h * G + j;
@@ -442,58 +486,53 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
       a.pl[(int64_t)hq * S + split] = den;
     }
   }
-  // the last block of this head merges every split into the output
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(&a.done[h], 1) == S - 1) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  float* m_sh = &s_m[0][0];
-  float* den_sh = &s_l[0][0];
-  // split scales: wave w takes heads w, w+4, ..; its lanes stride the splits
-  for (int j = wave; j < G; j += 4) {
-    const int hq = h * G + j;
-    const float* pm = a.pm + (int64_t)hq * S;
-    const float* pl = a.pl + (int64_t)hq * S;
+}
+
+// ----------------------------------------------------------------- merge ---
+// Block (query head, 64 dimensions): wave 0 finds the splits' common maximum
+// and scales, then each wave sums a quarter of the splits for its 64 dims.
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) {
+  __shared__ float s_sc[MAX_SPLITS];
+  __shared__ float s_red[4][64];
+  __shared__ float s_mu, s_den;
+  const int hq = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = blockIdx.y * 64 + lane;
+  const float* pm = a.pm + (int64_t)hq * S;
+  const float* pl = a.pl + (int64_t)hq * S;
+  if (wave == 0) {
     float mx = -INFINITY;
-    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, __builtin_nontemporal_load(pm + s));
-    mx = wave_max(mx);
+    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, pm[s]);
+    mx = wave_max_dpp(mx);
     const float mu = (mx == -INFINITY) ? 0.f : mx;
     float den = 0.f;
     for (int s = lane; s < S; s += 64) {
-      const float pmv = __builtin_nontemporal_load(pm + s);
+      const float pmv = pm[s];
       const float sc = (pmv == -INFINITY) ? 0.f : exp2f(pmv - mu);
-      s_scale[j][s] = sc;
-      den += __builtin_nontemporal_load(pl + s) * sc;
+      s_sc[s] = sc;
+      den += pl[s] * sc;
     }
-    den = wave_sum(den);
+    den = wave_sum_dpp(den);
     if (lane == 0) {
-      m_sh[j] = mu;
-      den_sh[j] = den;
+      s_mu = mu;
+      s_den = den;
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int j = e / D, d = e % D;
-    const int hq = h * G + j;
-    const float* src = a.pacc + (int64_t)hq * S * D + d;
-    float num0 = 0.f, num1 = 0.f, num2 = 0.f, num3 = 0.f;
-    int s = 0;
-    for (; s + 4 <= S; s += 4) {
-      num0 += __builtin_nontemporal_load(src + (int64_t)s * D) * s_scale[j][s];
-      num1 += __builtin_nontemporal_load(src + (int64_t)(s + 1) * D) * s_scale[j][s + 1];
-      num2 += __builtin_nontemporal_load(src + (int64_t)(s + 2) * D) * s_scale[j][s + 2];
-      num3 += __builtin_nontemporal_load(src + (int64_t)(s + 3) * D) * s_scale[j][s + 3];
-    }
-    for (; s < S; ++s) num0 += __builtin_nontemporal_load(src + (int64_t)s * D) * s_scale[j][s];
-    const float num = (num0 + num1) + (num2 + num3);
-    const float den = den_sh[j];
-    a.out[(int64_t)hq * a.out_sh + d] = f2bf(den == 0.f ? 0.f : num / den);
-    if (d == 0 && a.out_lse)
-      a.out_lse[hq] = (den > 0.f) ? (m_sh[j] + log2f(den)) * 0.69314718055994531f : -INFINITY;
+  const float* src = a.pacc + (int64_t)hq * S * D + d;
+  float num = 0.f;
+#pragma unroll 8
+  for (int s = wave; s < S; s += 4) num += src[(int64_t)s * D] * s_sc[s];
+  s_red[wave][lane] = num;
+  __syncthreads();
+  if (wave == 0) {
+    const float tot = (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
+    const float den = s_den;
+    a.out[(int64_t)hq * a.out_sh + d] = f2bf(den == 0.f ? 0.f : tot / den);
+    if (lane == 0 && blockIdx.y == 0 && a.out_lse)
+      a.out_lse[hq] = (den > 0.f) ? (s_mu + log2f(den)) * 0.69314718055994531f : -INFINITY;
   }
-  if (threadIdx.x == 0) a.done[h] = 0;
 }
 
 template <int D>
@@ -505,8 +544,16 @@ int launch_select(const DecodeArgs& a, hipStream_t stream) {
 
 template <int D, int G>
 int launch_attend(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attend_kernel<D, G>), dim3(a.Hkv, a.nsplit + a.ssplit), dim3(256), 0,
-                     stream, a);
+  const size_t lds = DecodeTile<D>::LDS_BYTES;
+  static bool configured = false;
+  if (!configured) {
+    hipFuncSetAttribute((const void*)decode_attend_kernel<D, G>,
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    configured = true;
+  }
+  const int S = a.nsplit + a.ssplit;
+  hipLaunchKernelGGL((decode_attend_kernel<D, G>), dim3(a.Hkv, S), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
   return SBSA_OK;
 }
 
@@ -580,7 +627,6 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   a.rcum = w + 2 * num_kv_heads * C;
   a.rcount = w + 3 * num_kv_heads * C;
   a.rtokens = a.rcount + num_kv_heads;
-  a.done = a.rtokens + num_kv_heads;
   const int S = num_splits + suffix_splits;
   a.pacc = (float*)(w + workspace_ints(num_kv_heads, C));
   a.pm = a.pacc + (size_t)num_q_heads * S * dim;

@@ -49,7 +49,8 @@ class SembloRuntimeConfig:
     kmeans_sample_size: int = 8192
     dense_prefix_x: int = 4                 # SEMBLO_FA3_DENSE_PREFIX_X
     iters: int = 16
-    decode_num_splits: int = 64             # prompt splits of the decode step
+    decode_num_splits: int = 56             # splits of the decode step (with the suffix splits:
+                                            # 64 blocks per KV head)
     decode_suffix_splits: int = 8           # SEMBLO_DECODE_SUFFIX_SPLITS
     suffix_block: int = 256
     suffix_reserve: int = 1024
