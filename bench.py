@@ -50,6 +50,8 @@ def _parse():
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=None)
     ap.add_argument("--decode-replays", type=int, default=5)
+    ap.add_argument("--decode-splits", type=int, default=None,
+                    help="splits per KV head of the decode step (default: the runtime config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-queries", type=int, default=64)
     ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
@@ -207,6 +209,8 @@ def main():
                         dtype=torch.bfloat16, device="cuda")
     cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
                               query_chunk_size=conf["chunk"], suffix_reserve=max(1024, dsteps + 16))
+    if args.decode_splits:
+        cfg.decode_num_splits = max(1, args.decode_splits - cfg.decode_suffix_splits)
     layer = SembloAttention(cfg, layer_name="bench.layer")
     result = {}
     if args.only in ("all", "prefill"):

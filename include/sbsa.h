@@ -187,9 +187,11 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
  * Hkv, dim] (through table, positions prompt_len..*pos), and the LSE merge
  * into out [Hq, dim] (row stride out_sh) and out_lse [Hq] (natural log, or
  * null).  q_pre holds pre-RoPE queries to route (router_pass 1) or routing
- * vectors already (router_pass 0).  pos is a device int.  num_splits +
- * suffix_splits <= 512.  No host reads, no allocation: capturable in a
- * HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
+ * vectors already (router_pass 0).  pos is a device int.  The suffix holds at
+ * most 16*max_tiles positions from prompt_len (max_tiles 0: no suffix), and
+ * table maps logical blocks prompt_len/suffix_block through
+ * (prompt_len + 16*max_tiles - 1)/suffix_block.  num_splits + suffix_splits
+ * <= 512.  No host reads, no allocation: capturable in a HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
  * then rcount [Hkv] and rtokens [Hkv]. */
 size_t sbsa_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int num_clusters, int dim,
                                    int num_splits, int suffix_splits);

@@ -8,20 +8,21 @@
 //                             suffix splits via the block table)
 //   fused_decode.py:334-358   _decode_merge_kernel
 //
-// Three launches, no host reads, no allocation: every size the kernels need
+// Two launches, no host reads, no allocation: every size the kernels need
 // (the position, the selected token count) is read on the device, so a HIP
 // graph can capture the step and replay it at fixed addresses.
-//   1. select: one block per KV head -- routing, scores on MFMA, per-component
-//      LSE, bisection under the budget and the CSR of the selection (wave 0),
-//      while the other waves write the token's K/V into the suffix store.
-//   2. attend: one block per (KV head, split).  A head's keys are one list,
-//      the selected prompt rows (in CSR order) followed by the live suffix
-//      rows; each split takes an even, 32-aligned range of it.  The block
-//      resolves its rows' addresses into LDS, each wave gathers 32-key tiles
-//      straight into LDS (global loads to LDS) and runs S^T = K Q^T and
+//   1. step: one block per (KV head, split).  Every block first selects for
+//      its head (routing, scores on MFMA, per-component LSE, bisection under
+//      the budget, the CSR of the selection into LDS); split 0 also writes
+//      the CSR to the workspace and the token's K/V into the suffix store.
+//      A head's keys are one list, the selected prompt rows in CSR order
+//      followed by the live suffix rows (the current token's row read from
+//      k_new/v_new); each split takes an even, 32-aligned range of it.  The
+//      block resolves its rows' addresses into LDS, each wave gathers 32-key
+//      tiles straight into LDS (global loads to LDS) and runs S^T = K Q^T and
 //      O^T = V^T P^T on MFMA with the G query heads as columns; the waves'
 //      partials are folded in LDS into the split's partial.
-//   3. merge: one block per (query head, 64 dimensions) folds the splits.
+//   2. merge: one block per (query head, 64 dimensions) folds the splits.
 #include "sbsa_common.h"
 
 namespace {
@@ -64,32 +65,72 @@ struct DecodeArgs {
 
 constexpr int MAX_C = 1024;
 constexpr int MAX_SPLITS = 512;   // prompt + suffix splits of one step
+constexpr int DT = 32;            // keys per wave tile
+constexpr int ROW_CHUNK = 256;    // rows whose addresses a block resolves at once
+constexpr int MAX_TABLE = 256;    // suffix block-table entries staged in LDS
 
-// ---------------------------------------------------------------- select ---
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// Per-wave LDS tile: DT rows of K then DT rows of V, each row D bf16 with
+// its 16-byte chunks permuted (K: chunk ^ (row % 8), V: chunk ^ 2 (row % 4))
+// so that the MFMA operand reads spread over the banks.
 template <int D>
-__global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
+struct DecodeTile {
+  static constexpr int ROW_BYTES = 2 * D;
+  static constexpr int CH = D / 8;               // 16-byte chunks per row
+  static constexpr int RPI = 64 / CH;            // rows per wave load instruction
+  static constexpr int INSTS = DT / RPI;         // load instructions per K (or V) tile
+  static constexpr int KV_BYTES = DT * ROW_BYTES;
+  static constexpr int WAVE_BYTES = 2 * KV_BYTES;
+  static constexpr size_t STAGE_BYTES = 4 * (size_t)WAVE_BYTES;
+};
+
+// Dynamic LDS of the step kernel: the tile staging, or the selection's
+// routing vectors [16][D+8] bf16 and component weights [G][C] f32.
+template <int D>
+size_t step_lds_bytes(int G, int C) {
+  size_t sel = (size_t)16 * (D + 8) * 2 + (size_t)G * C * 4;
+  return sel > DecodeTile<D>::STAGE_BYTES ? sel : DecodeTile<D>::STAGE_BYTES;
+}
+
+// ------------------------------------------------------------- selection ---
+// All 256 threads.  NK = clusters per lane of wave 0 (C <= 64 NK).  Leaves
+// the CSR of the head's selection in s_rstart / s_rcum (rcount entries) and
+// s_cnt = {rcount, rtokens}.
+template <int D, int NK, typename Prefetch>
+__device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, int pos_v,
+                                             Prefetch prefetch, unsigned char* smem, int* s_rstart,
+                                             int* s_rcum, int* s_cnt) {
   constexpr int KS = D / 32;
   constexpr int LDQ = D + 8;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   bf16_t* svec = reinterpret_cast<bf16_t*>(smem);                   // [16][LDQ]
   float* ssc = reinterpret_cast<float*>(smem + 16 * LDQ * 2);        // [G][C]
-  const int h = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int C = a.C, G = a.G;
   const int half = D / 2;
   const int nk = C / 64;
+  constexpr int PER = D / 64;
 
-  // loads that depend on nothing, issued first
-  int sz[16], ip[16];
-  if (wave == 0) {
+  // loads in the order of use: the router input row of this wave's first
+  // head (raw bits, converted at the routing), the codebook tiles, then the
+  // caller's.  Wave 0 copies the sizes and run starts straight into LDS
+  // (s_rcum / s_rstart, rewritten with the CSR later).
+  uint32_t vq[PER];
+  if (wave < G) {
+    const bf16_t* src = a.q_pre + (int64_t)(h * G + wave) * a.qp_sh;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      sz[k] = (k < nk) ? a.sizes[h * C + lane + 64 * k] : 0;
-      ip[k] = (k < nk) ? a.indptr[h * (C + 1) + lane + 64 * k] : 0;
+    for (int i = 0; i < PER; ++i) vq[i] = src[lane + 64 * i];
+  }
+  if (wave == 0) {
+    for (int k = 0; k < nk; ++k) {
+      __builtin_amdgcn_global_load_lds((const void*)(a.sizes + h * C + 64 * k + lane),
+                                       (lds_void_t*)(s_rcum + 64 * k), 4, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(a.indptr + h * (C + 1) + 64 * k + lane),
+                                       (lds_void_t*)(s_rstart + 64 * k), 4, 0, 0);
     }
   }
-  const int64_t q_pos = *a.pos;   // used by the suffix write at the end
-  // the first two codebook tiles of this wave, in flight during the routing
   const bf16_t* cb = a.codebooks + (int64_t)h * 2 * C * half;
   auto load_cb = [&](int cbk, u32x4_t* b) {
     const int cc = cbk * 16 + (lane & 15);
@@ -100,23 +141,26 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       b[s] = *reinterpret_cast<const u32x4_t*>(cb + ((int64_t)part * C + cc) * half + (d - part * half));
     }
   };
+  // the first two codebook tiles of this wave, in flight during the routing
   u32x4_t b0[KS], b1[KS];
   if (wave < C / 16) load_cb(wave, b0);
   if (wave + 4 < C / 16) load_cb(wave + 4, b1);
+  prefetch();
   // 1. routing vectors of the G query heads (rows >= G are zero)
   for (int e = threadIdx.x; e < 16 * (D / 8); e += 256) {
     int r = e / (D / 8), ch = e % (D / 8);
     if (r >= G) *reinterpret_cast<u32x4_t*>(&svec[r * LDQ + ch * 8]) = u32x4_t{0, 0, 0, 0};
   }
+  // keeps the first row's conversion here, after the codebook loads were issued
+#pragma unroll
+  for (int i = 0; i < PER; ++i) asm volatile("" : "+v"(vq[i]));
   for (int t = wave; t < G; t += 4) {
     const bf16_t* src = a.q_pre + (int64_t)(h * G + t) * a.qp_sh;
-    constexpr int PER = (D + 63) / 64;
     float v[PER];
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      int d = lane + 64 * i;
-      v[i] = d < D ? bf2f(src[d]) : 0.f;
+      v[i] = bf2f((t == wave) ? (bf16_t)vq[i] : src[lane + 64 * i]);
       ss += v[i] * v[i];
     }
     if (a.router_pass) {
@@ -132,10 +176,7 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
       for (int i = 0; i < PER; ++i) v[i] = v[i] / n2;
     }
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      int d = lane + 64 * i;
-      if (d < D) svec[t * LDQ + d] = f2bf(v[i]);
-    }
+    for (int i = 0; i < PER; ++i) svec[t * LDQ + lane + 64 * i] = f2bf(v[i]);
   }
   __syncthreads();
   // 2. scores s[t][c] = v_t . c / tau on MFMA (16 rows, G real)
@@ -169,16 +210,18 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
     for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
     m = wave_max_dpp(m);
     float l = 0.f;
-    for (int c = lane; c < C; c += 64) l += expf(row[c] - m);
+    constexpr float LOG2E = 1.4426950408889634f;
+    for (int c = lane; c < C; c += 64) l += __builtin_amdgcn_exp2f((row[c] - m) * LOG2E);
     l = wave_sum_dpp(l);
-    float lse = m + logf(l);
-    for (int c = lane; c < C; c += 64) row[c] = expf(row[c] - lse);
+    const float lse2 = m * LOG2E + __builtin_amdgcn_logf(l);    // log2 of the normaliser
+    for (int c = lane; c < C; c += 64) row[c] = __builtin_amdgcn_exp2f(__builtin_fmaf(row[c], LOG2E, -lse2));
   }
   __syncthreads();
   if (wave != 0) {
-    // the token's K/V into the suffix store (a position past the reservation
-    // is not written: the table does not cover it)
-    if (a.k_new && q_pos >= a.prompt_len && q_pos - a.prompt_len < (int64_t)a.max_tiles * 16) {
+    // the token's K/V into the suffix store, once per head (a position past
+    // the reservation is not written: the table does not cover it)
+    const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
+    if (leader && a.k_new && q_pos >= a.prompt_len && q_pos - a.prompt_len < (int64_t)a.max_tiles * 16) {
       const int64_t blk = q_pos / a.BS;
       const int64_t off = q_pos - blk * a.BS;
       const int64_t phys = a.table[blk];
@@ -189,111 +232,126 @@ __global__ __launch_bounds__(256) void decode_select_kernel(DecodeArgs a) {
         dst[plane + d] = a.v_new[(int64_t)h * a.kn_sh + d];
       }
     }
-    return;
-  }
-  // 4. bisection and CSR emission (wave 0); sizes are integers below 2^24, so
-  //    the reference's fp32 sums are exact and equal these integer sums
-  const float NEG = -3.4e38f, POS = 3.4e38f;
-  float score[16];
-  int size[16];
-  float hi = -INFINITY, lo = INFINITY;
-  int live_total = 0;
+  } else {
+    // 4. bisection and the CSR (wave 0); sizes are integers below 2^24, so
+    //    the reference's fp32 sums are exact and equal these integer sums
+    __builtin_amdgcn_s_waitcnt(0);       // this wave's copies into LDS have landed
+    int sz[NK], ip[NK];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    score[k] = NEG;
-    size[k] = 0;
-    if (k < nk) {
-      const int c = lane + 64 * k;
-      float p = 0.f;
-      for (int t = 0; t < G; ++t) p += ssc[t * C + c];
-      const int s = (a.sink > 0 && c == 0) ? 0 : sz[k];
-      size[k] = s;
-      const bool live = s > 0;
-      float sc = logf(fmaxf(p, 1e-38f));
-      if (a.beta != 0.f) sc = sc - a.beta * logf(1.0f + (float)s);
-      sc = live ? sc : NEG;
-      score[k] = sc;
-      hi = fmaxf(hi, sc);
-      lo = fminf(lo, live ? sc : POS);
-      live_total += live ? s : 0;
+    for (int k = 0; k < NK; ++k) {
+      sz[k] = (k < nk) ? s_rcum[lane + 64 * k] : 0;
+      ip[k] = (k < nk) ? s_rstart[lane + 64 * k] : 0;
     }
-  }
-  hi = wave_max_dpp(hi) + 1e-6f;
-  lo = wave_min_dpp(lo) - 1e-6f;
-  lo = fminf(lo, hi - 1e-5f);
-  live_total = wave_sum_i32_dpp(live_total);
-  const float budget = (a.sink > 0) ? fmaxf(a.target - (float)a.sink, 0.f) : a.target;
-  const bool all_fit = (float)live_total < budget;
-  for (int it = 0; it < a.iters; ++it) {
-    const float mid = (lo + hi) * 0.5f;
-    int above = 0;
+    const float NEG = -3.4e38f, POS = 3.4e38f;
+    float score[NK];
+    int size[NK];
+    float hi = -INFINITY, lo = INFINITY;
+    int live_total = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-      if (k < nk && score[k] >= mid) above += size[k];
-    above = wave_sum_i32_dpp(above);
-    const bool reach = (float)above >= budget;
-    lo = reach ? mid : lo;
-    hi = reach ? hi : mid;
-  }
-  const float theta = all_fit ? NEG : lo;
-  int carry_n = 0, carry_tok = 0;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (k < nk) {
-      const int c = lane + 64 * k;
-      const bool sel = (size[k] > 0 && score[k] >= theta) || (a.sink > 0 && c == 0 && sz[k] > 0);
-      const int si = sel ? 1 : 0;
-      const int sl = sel ? sz[k] : 0;
-      const int pi = wave_incl_scan_dpp(si);
-      const int pt = wave_incl_scan_dpp(sl);
-      if (sel) {
-        const int p = carry_n + pi - 1;
-        a.rstart[h * C + p] = ip[k];
-        a.rlen[h * C + p] = sl;
-        a.rcum[h * C + p] = carry_tok + pt - sl;
+    for (int k = 0; k < NK; ++k) {
+      score[k] = NEG;
+      size[k] = 0;
+      if (k < nk) {
+        const int c = lane + 64 * k;
+        float p = 0.f;
+        for (int t = 0; t < G; ++t) p += ssc[t * C + c];
+        const int s = (a.sink > 0 && c == 0) ? 0 : sz[k];
+        size[k] = s;
+        const bool live = s > 0;
+        float sc = logf(fmaxf(p, 1e-38f));
+        if (a.beta != 0.f) sc = sc - a.beta * logf(1.0f + (float)s);
+        sc = live ? sc : NEG;
+        score[k] = sc;
+        hi = fmaxf(hi, sc);
+        lo = fminf(lo, live ? sc : POS);
+        live_total += live ? s : 0;
       }
-      carry_n += __builtin_amdgcn_readlane(pi, 63);
-      carry_tok += __builtin_amdgcn_readlane(pt, 63);
+    }
+    hi = wave_max_dpp(hi) + 1e-6f;
+    lo = wave_min_dpp(lo) - 1e-6f;
+    lo = fminf(lo, hi - 1e-5f);
+    live_total = wave_sum_i32_dpp(live_total);
+    const float budget = (a.sink > 0) ? fmaxf(a.target - (float)a.sink, 0.f) : a.target;
+    const bool all_fit = (float)live_total < budget;
+    // two bisection steps per round: the first step's mid and both possible
+    // second mids are counted together (the same fp32 mids as one step at a time)
+    for (int it = 0; it < a.iters; it += 2) {
+      const float m0 = (lo + hi) * 0.5f;
+      const float m1 = (m0 + hi) * 0.5f;     // second mid if m0 reaches the budget
+      const float m2 = (lo + m0) * 0.5f;     // second mid otherwise
+      int c0 = 0, c1 = 0, c2 = 0;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        c0 += score[k] >= m0 ? size[k] : 0;
+        c1 += score[k] >= m1 ? size[k] : 0;
+        c2 += score[k] >= m2 ? size[k] : 0;
+      }
+      wave_sum3_i32_dpp(c0, c1, c2);
+      if ((float)c0 >= budget) {
+        lo = m0;
+        if (it + 1 < a.iters) {
+          if ((float)c1 >= budget) lo = m1;
+          else hi = m1;
+        }
+      } else {
+        hi = m0;
+        if (it + 1 < a.iters) {
+          if ((float)c2 >= budget) lo = m2;
+          else hi = m2;
+        }
+      }
+    }
+    const float theta = all_fit ? NEG : lo;
+    int carry_n = 0, carry_tok = 0;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      if (k < nk) {
+        const int c = lane + 64 * k;
+        const bool sel = (size[k] > 0 && score[k] >= theta) || (a.sink > 0 && c == 0 && sz[k] > 0);
+        const int si = sel ? 1 : 0;
+        const int sl = sel ? sz[k] : 0;
+        const int pi = wave_incl_scan_dpp(si);
+        const int pt = wave_incl_scan_dpp(sl);
+        if (sel) {
+          const int p = carry_n + pi - 1;
+          const int cum = carry_tok + pt - sl;
+          s_rstart[p] = ip[k];
+          s_rcum[p] = cum;
+          if (leader) {
+            a.rstart[h * C + p] = ip[k];
+            a.rlen[h * C + p] = sl;
+            a.rcum[h * C + p] = cum;
+          }
+        }
+        carry_n += __builtin_amdgcn_readlane(pi, 63);
+        carry_tok += __builtin_amdgcn_readlane(pt, 63);
+      }
+    }
+    if (lane == 0) {
+      s_cnt[0] = carry_n;
+      s_cnt[1] = carry_tok;
+      if (leader) {
+        a.rcount[h] = carry_n;
+        a.rtokens[h] = carry_tok;
+      }
     }
   }
-  if (lane == 0) {
-    a.rcount[h] = carry_n;
-    a.rtokens[h] = carry_tok;
-  }
+  __syncthreads();
 }
 
-// ---------------------------------------------------------------- attend ---
-constexpr int DT = 32;          // keys per wave tile
-constexpr int ROW_CHUNK = 256;  // rows whose addresses a block resolves at once
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((ext_vector_type(4))) short s16x4_t;
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-
-// Per-wave LDS tile: DT rows of K then DT rows of V, each row D bf16 with
-// its 16-byte chunks permuted (K: chunk ^ (row % 8), V: chunk ^ 2 (row % 4))
-// so that the MFMA operand reads spread over the banks.
-template <int D>
-struct DecodeTile {
-  static constexpr int ROW_BYTES = 2 * D;
-  static constexpr int CH = D / 8;               // 16-byte chunks per row
-  static constexpr int RPI = 64 / CH;            // rows per wave load instruction
-  static constexpr int INSTS = DT / RPI;         // load instructions per K (or V) tile
-  static constexpr int KV_BYTES = DT * ROW_BYTES;
-  static constexpr int WAVE_BYTES = 2 * KV_BYTES;
-  static constexpr size_t LDS_BYTES = 4 * (size_t)WAVE_BYTES;
-};
-
-template <int D, int G>
-__global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
+// ------------------------------------------------------------------ step ---
+template <int D, int G, int NK>
+__global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
   using T = DecodeTile<D>;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
   static_assert(G <= 16, "query heads per KV head");
-  static_assert(16 * G * D <= (int)T::LDS_BYTES, "wave partials fit the tile space");
+  static_assert(16 * G * D <= (int)T::STAGE_BYTES, "wave partials fit the tile space");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_dec[];
   __shared__ int s_rcum[MAX_C];
   __shared__ int s_rstart[MAX_C];
+  __shared__ int s_cnt[2];
+  __shared__ int s_table[MAX_TABLE];
   __shared__ const bf16_t* s_kaddr[ROW_CHUNK];
   __shared__ const bf16_t* s_vaddr[ROW_CHUNK];
   __shared__ float s_m[4][16];
@@ -303,33 +361,44 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   const int S = gridDim.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
+  // the position as a vector load (a scalar load would be waited on by the
+  // first LDS access)
+  const int pos_v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // suffix block table entries the live suffix may use (at most MAX_TABLE)
+  const int64_t tb0 = a.prompt_len / a.BS;
+  const int64_t tb_n = a.max_tiles > 0 ? (a.prompt_len + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
+  const bool table_in_lds = tb_n <= MAX_TABLE;
+  if (table_in_lds && wave == 0)   // copied straight into LDS; waited on in the selection
+    for (int k = 0; k * 64 < tb_n; ++k)
+      if (k * 64 + lane < tb_n)
+        __builtin_amdgcn_global_load_lds((const void*)(a.table + tb0 + k * 64 + lane),
+                                         (lds_void_t*)(s_table + 64 * k), 4, 0, 0);
+
+  // Q^T as the B operand: column l16 is query head h*G + l16 (zero past G);
+  // in flight during the selection
+  u32x4_t qr[KS];
+  auto load_q = [&]() {
+    const bool ok = l16 < G;
+    const bf16_t* src = a.q_post + (int64_t)(h * G + (ok ? l16 : 0)) * a.q_sh + lg * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
+  };
+
+  select_phase<D, NK>(a, h, split == 0, pos_v, load_q, smem_dec, s_rstart, s_rcum, s_cnt);
+  const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
 
   // this split's range of the head's key list (prompt rows, then suffix rows)
-  const int64_t q_pos = *a.pos;
-  const int count = a.rtokens[h];
-  const int rcount = a.rcount[h];
+  const int rcount = s_cnt[0];
+  const int count = s_cnt[1];
   int64_t nsuf64 = q_pos - a.prompt_len + 1;
   nsuf64 = nsuf64 < 0 ? 0 : (nsuf64 > (int64_t)a.max_tiles * 16 ? (int64_t)a.max_tiles * 16 : nsuf64);
   const int total = count + (int)nsuf64;
   const int per = ((total + S - 1) / S + DT - 1) / DT * DT;
   const int r_lo = min(split * per, total);
   const int r_hi = min(r_lo + per, total);
-  for (int i = threadIdx.x; i < rcount; i += 256) {
-    s_rcum[i] = a.rcum[h * a.C + i];
-    s_rstart[i] = a.rstart[h * a.C + i];
-  }
   const int64_t pplane = a.packed_len * a.Hkv * D;
   const int64_t splane = a.suffix_nblk * a.BS * a.Hkv * D;
-
-  // Q^T as the B operand: column l16 is query head h*G + l16 (zero past G)
-  u32x4_t qr[KS];
-  {
-    const bool ok = l16 < G;
-    const bf16_t* src = a.q_post + (int64_t)(h * G + (ok ? l16 : 0)) * a.q_sh + lg * 8;
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
-  }
 
   // fixed per-lane LDS offsets
   const int cpos = lane % T::CH;
@@ -348,7 +417,6 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   f32x4_t o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = f32x4_t{0, 0, 0, 0};
-  __syncthreads();
 
   for (int c0 = r_lo; c0 < r_hi; c0 += ROW_CHUNK) {
     const int cn = min(ROW_CHUNK, r_hi - c0);
@@ -356,7 +424,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
       // address of row c0 + tid of the key list (rows past cn: a valid dummy row)
       const int oo = c0 + (int)threadIdx.x;
       const bf16_t* kp = a.packed + (int64_t)h * D;
-      int64_t vo = pplane;
+      const bf16_t* vp = kp + pplane;
       if ((int)threadIdx.x < cn) {
         if (oo < count) {
           int lo = 0, hi = rcount;
@@ -368,17 +436,23 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
           const int r = lo > 0 ? lo - 1 : 0;
           const int64_t row = (int64_t)s_rstart[r] + (oo - s_rcum[r]);
           kp = a.packed + (row * a.Hkv + h) * D;
+          vp = kp + pplane;
         } else {
           const int64_t p = a.prompt_len + (oo - count);
-          const int64_t blk = p / a.BS;
-          const int64_t off = p - blk * a.BS;
-          const int64_t phys = a.table[blk];
-          kp = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
-          vo = splane;
+          if (a.k_new && p == q_pos) {
+            kp = a.k_new + (int64_t)h * a.kn_sh;
+            vp = a.v_new + (int64_t)h * a.kn_sh;
+          } else {
+            const int64_t blk = p / a.BS;
+            const int64_t off = p - blk * a.BS;
+            const int64_t phys = table_in_lds ? (int64_t)s_table[blk - tb0] : (int64_t)a.table[blk];
+            kp = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
+            vp = kp + splane;
+          }
         }
       }
       s_kaddr[threadIdx.x] = kp;
-      s_vaddr[threadIdx.x] = kp + vo;
+      s_vaddr[threadIdx.x] = vp;
     }
     __syncthreads();
     for (int t0 = wave * DT; t0 < cn; t0 += 4 * DT) {
@@ -489,72 +563,88 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
 }
 
 // ----------------------------------------------------------------- merge ---
-// Block (query head, 64 dimensions): wave 0 finds the splits' common maximum
-// and scales, then each wave sums a quarter of the splits for its 64 dims.
+// Block (query head, 64 dimensions); wave w sums splits w, w+4, ... of its 64
+// dims.  The partials are loaded first; every wave derives the splits' common
+// maximum and scales itself (no block barrier before the sums).
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) {
-  __shared__ float s_sc[MAX_SPLITS];
+  constexpr int PRE = 16;                 // splits per wave loaded up front
+  __shared__ float s_sc[4][MAX_SPLITS];
   __shared__ float s_red[4][64];
-  __shared__ float s_mu, s_den;
   const int hq = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int d = blockIdx.y * 64 + lane;
+  const float* src = a.pacc + (int64_t)hq * S * D + d;
+  float v[PRE];
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int s = wave + 4 * i;
+    v[i] = s < S ? src[(int64_t)s * D] : 0.f;
+  }
   const float* pm = a.pm + (int64_t)hq * S;
   const float* pl = a.pl + (int64_t)hq * S;
-  if (wave == 0) {
-    float mx = -INFINITY;
-    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, pm[s]);
-    mx = wave_max_dpp(mx);
-    const float mu = (mx == -INFINITY) ? 0.f : mx;
-    float den = 0.f;
-    for (int s = lane; s < S; s += 64) {
-      const float pmv = pm[s];
-      const float sc = (pmv == -INFINITY) ? 0.f : exp2f(pmv - mu);
-      s_sc[s] = sc;
-      den += pl[s] * sc;
-    }
-    den = wave_sum_dpp(den);
-    if (lane == 0) {
-      s_mu = mu;
-      s_den = den;
-    }
+  constexpr int PS = MAX_SPLITS / 64;
+  float pmv[PS], plv[PS];
+#pragma unroll
+  for (int k = 0; k < PS; ++k) {
+    const int s = lane + 64 * k;
+    pmv[k] = s < S ? pm[s] : -INFINITY;
+    plv[k] = s < S ? pl[s] : 0.f;
   }
-  __syncthreads();
-  const float* src = a.pacc + (int64_t)hq * S * D + d;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < PS; ++k) mx = fmaxf(mx, pmv[k]);
+  mx = wave_max_dpp(mx);
+  const float mu = (mx == -INFINITY) ? 0.f : mx;
+  float den = 0.f;
+#pragma unroll
+  for (int k = 0; k < PS; ++k) {
+    const int s = lane + 64 * k;
+    const float sc = (pmv[k] == -INFINITY) ? 0.f : exp2f(pmv[k] - mu);
+    if (s < S) s_sc[wave][s] = sc;
+    den += plv[k] * sc;
+  }
+  den = wave_sum_dpp(den);
+  __builtin_amdgcn_wave_barrier();
   float num = 0.f;
-#pragma unroll 8
-  for (int s = wave; s < S; s += 4) num += src[(int64_t)s * D] * s_sc[s];
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int s = wave + 4 * i;
+    if (s < S) num += v[i] * s_sc[wave][s];
+  }
+  for (int s = wave + 4 * PRE; s < S; s += 4) num += src[(int64_t)s * D] * s_sc[wave][s];
   s_red[wave][lane] = num;
   __syncthreads();
   if (wave == 0) {
     const float tot = (s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane]);
-    const float den = s_den;
     a.out[(int64_t)hq * a.out_sh + d] = f2bf(den == 0.f ? 0.f : tot / den);
     if (lane == 0 && blockIdx.y == 0 && a.out_lse)
-      a.out_lse[hq] = (den > 0.f) ? (s_mu + log2f(den)) * 0.69314718055994531f : -INFINITY;
+      a.out_lse[hq] = (den > 0.f) ? (mu + log2f(den)) * 0.69314718055994531f : -INFINITY;
   }
 }
 
-template <int D>
-int launch_select(const DecodeArgs& a, hipStream_t stream) {
-  size_t lds = 16 * (D + 8) * 2 + (size_t)a.G * a.C * 4;
-  hipLaunchKernelGGL(decode_select_kernel<D>, dim3(a.Hkv), dim3(256), lds, stream, a);
+template <int D, int G, int NK>
+int launch_step(const DecodeArgs& a, hipStream_t stream) {
+  const size_t lds = step_lds_bytes<D>(G, a.C);
+  static size_t configured = 0;
+  if (lds > configured) {
+    if (hipFuncSetAttribute((const void*)decode_step_kernel<D, G, NK>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return SBSA_ERR_UNSUPPORTED;
+    configured = lds;
+  }
+  const int S = a.nsplit + a.ssplit;
+  hipLaunchKernelGGL((decode_step_kernel<D, G, NK>), dim3(a.Hkv, S), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
   return SBSA_OK;
 }
 
 template <int D, int G>
-int launch_attend(const DecodeArgs& a, hipStream_t stream) {
-  const size_t lds = DecodeTile<D>::LDS_BYTES;
-  static bool configured = false;
-  if (!configured) {
-    hipFuncSetAttribute((const void*)decode_attend_kernel<D, G>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    configured = true;
-  }
-  const int S = a.nsplit + a.ssplit;
-  hipLaunchKernelGGL((decode_attend_kernel<D, G>), dim3(a.Hkv, S), dim3(256), lds, stream, a);
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
-  return SBSA_OK;
+int launch_step_nk(const DecodeArgs& a, hipStream_t stream) {
+  if (a.C <= 64) return launch_step<D, G, 1>(a, stream);
+  if (a.C <= 128) return launch_step<D, G, 2>(a, stream);
+  if (a.C <= 256) return launch_step<D, G, 4>(a, stream);
+  return launch_step<D, G, 16>(a, stream);
 }
 
 size_t workspace_ints(int num_kv_heads, int num_clusters) {
@@ -590,7 +680,7 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   if ((k_new == nullptr) != (v_new == nullptr)) return SBSA_ERR_ARG;
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_splits < 1 || suffix_splits < 1)
     return SBSA_ERR_ARG;
-  if (q_sh % 8 || qp_sh % 8) return SBSA_ERR_ARG;
+  if (q_sh % 8 || qp_sh % 8 || kn_sh % 8 || max_tiles < 0) return SBSA_ERR_ARG;
   const int G = num_q_heads / num_kv_heads;
   const int C = num_clusters;
   if (C % 64 || C > MAX_C) return SBSA_ERR_UNSUPPORTED;
@@ -648,11 +738,7 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   a.target = target_tokens;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   int rc = SBSA_ERR_UNSUPPORTED;
-  if (dim == 128) rc = launch_select<128>(a, stream);
-  else if (dim == 256) rc = launch_select<256>(a, stream);
-  if (rc) return rc;
-  rc = SBSA_ERR_UNSUPPORTED;
-#define SBSA_ATT(D_, G_) if (dim == D_ && G == G_) rc = launch_attend<D_, G_>(a, stream);
+#define SBSA_ATT(D_, G_) if (dim == D_ && G == G_) rc = launch_step_nk<D_, G_>(a, stream);
   SBSA_ATT(128, 1) SBSA_ATT(128, 2) SBSA_ATT(128, 4) SBSA_ATT(128, 8)
   SBSA_ATT(256, 1) SBSA_ATT(256, 2) SBSA_ATT(256, 4) SBSA_ATT(256, 8)
 #undef SBSA_ATT

@@ -139,6 +139,19 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_f<0x128>(v);
   return ((readlane_f(v, 0) + readlane_f(v, 16)) + readlane_f(v, 32)) + readlane_f(v, 48);
 }
+// three independent integer sums over a wave, interleaved
+__device__ __forceinline__ void wave_sum3_i32_dpp(int& x, int& y, int& z) {
+  x += dpp_i<0xB1>(x); y += dpp_i<0xB1>(y); z += dpp_i<0xB1>(z);
+  x += dpp_i<0x4E>(x); y += dpp_i<0x4E>(y); z += dpp_i<0x4E>(z);
+  x += dpp_i<0x124>(x); y += dpp_i<0x124>(y); z += dpp_i<0x124>(z);
+  x += dpp_i<0x128>(x); y += dpp_i<0x128>(y); z += dpp_i<0x128>(z);
+  x = (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
+      (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
+  y = (__builtin_amdgcn_readlane(y, 0) + __builtin_amdgcn_readlane(y, 16)) +
+      (__builtin_amdgcn_readlane(y, 32) + __builtin_amdgcn_readlane(y, 48));
+  z = (__builtin_amdgcn_readlane(z, 0) + __builtin_amdgcn_readlane(z, 16)) +
+      (__builtin_amdgcn_readlane(z, 32) + __builtin_amdgcn_readlane(z, 48));
+}
 // inclusive prefix sum over the wave (row scans by row_shr, then row carries)
 __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
   v += dpp_i<0x111>(v);

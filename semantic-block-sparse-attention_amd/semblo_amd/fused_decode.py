@@ -97,7 +97,7 @@ class _PromptOnly:
         self.suffix_block = 256
         self.suffix_table = torch.zeros(1, dtype=torch.int32, device=device)
         self.prompt_length = 1 << 40
-        self.max_tiles = 1
+        self.max_tiles = 0
         self.suffix_splits = 1
 
 
@@ -119,7 +119,7 @@ def decode_prompt_only(q_chunk: torch.Tensor, vectors: torch.Tensor, index, *, t
     _lib.call("sbsa_decode_step", _lib.ptr(q), d, _lib.ptr(v), d, 0, None, None, 0, _lib.ptr(pos),
               _lib.ptr(holder.codebooks), _lib.ptr(holder.sizes), _lib.ptr(holder.indptr),
               _lib.ptr(holder.packed_kv), holder.packed_kv.shape[1], _lib.ptr(holder.suffix_kv), 1,
-              256, _lib.ptr(holder.suffix_table), holder.prompt_length, 1, hq, hkv,
+              256, _lib.ptr(holder.suffix_table), holder.prompt_length, holder.max_tiles, hq, hkv,
               index.num_buckets, d, 1.0 / float(temperature), float(beta), float(target_tokens),
               int(iters), 0, float(sm_scale), int(num_splits), 1, _lib.ptr(ws.buffer), ws.nbytes,
               _lib.ptr(out), d, _lib.ptr(lse), None, _lib.stream(dev))
