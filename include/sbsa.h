@@ -132,6 +132,11 @@ int sbsa_reverse_index(const int32_t* qmask, int num_queries, int num_kv_heads, 
                        int64_t* nnz, int32_t* qvals, int64_t qvals_cap, int32_t* qrank,
                        hipStream_t stream);
 
+/* (query, head) rows of one prefill work item: the host tiles each (head,
+ * cluster) query list into items of sbsa_prefill_item_rows() / G queries.
+ * No counterpart in the reference (its FA3 calls take whole lists). */
+int sbsa_prefill_item_rows(void);
+
 /* ---- S5: KV-outer prefill attention ---------------------------------------------
  * The work list replacing the per-(cluster, KV head) FA3 varlen calls and the
  * local-window call of kv_outer_attention (semblo/vllm_plugin/kv_outer.py:661-753).
@@ -155,7 +160,7 @@ int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clus
  * causally.  Cluster partials: part_o [nnz, G, dim] bf16, part_lse [nnz, G];
  * the local window: local_o [Qc, Hq, dim] (strides lo_sq, lo_sh) and
  * local_lse [Qc, Hq] (null for a dense chunk, whose local_o is the output).
- * grid: persistent blocks (<= 0 picks a default).  dim in {128, 256}, Hq/Hkv
+ * grid: persistent blocks (<= 0: as many as the device holds at once).  dim in {128, 256}, Hq/Hkv
  * in {1, 2, 4, 8}. */
 int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queries,
                         int num_q_heads, int num_kv_heads, int dim, const void* packed,

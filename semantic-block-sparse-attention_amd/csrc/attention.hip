@@ -44,11 +44,14 @@ struct AttnArgs {
   float scale_log2;         // sm_scale * log2(e)
 };
 
-constexpr int KT = 64;      // keys per tile
-// A row's running maximum is only raised (and the accumulators rescaled) when
-// a tile's maximum exceeds it by more than this (log2 units): probabilities
-// stay below 2^8, and most tiles skip the rescale of the accumulators.
-constexpr float RESCALE_LOG2 = 8.0f;
+constexpr int KT = 32;      // keys per tile
+constexpr int PREFILL_RB = 2;                       // 16-row blocks per wave
+constexpr int PREFILL_ROWS = 4 * 16 * PREFILL_RB;   // (query, head) rows per work item
+constexpr int KB = KT / 16; // 16-key blocks per tile
+constexpr int T2 = KT / 32; // 32-key MFMA steps of O^T += V^T P^T per tile
+// Probabilities are taken against a reference maximum per row and may reach
+// 2^OVERFLOW_LOG2 (well inside fp32 and bf16 range) before an item is redone.
+constexpr float OVERFLOW_LOG2 = 64.0f;
 constexpr int BUFFER_CONFIG = 0x00020000;   // raw buffer resource, 32-bit data format
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
@@ -56,8 +59,10 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 // LDS tile layout: K and V rows of D bf16, row-major; the 16-byte chunks of
-// row r are permuted by an XOR (K: chunk ^ (r % 8), V: chunk ^ 2 (r % 4)) so
-// that the MFMA operand reads hit distinct banks.  Tiles are filled straight
+// row r are permuted by an XOR (K: chunk ^ (r % 16), V: chunk ^ 2 (r % 8)) so
+// that the MFMA operand reads of one LDS cycle (16 lanes of 16 bytes for K,
+// 32 lanes of 8 bytes for the transposing V reads: 256 bytes, the 64 banks)
+// hit distinct banks.  Tiles are filled straight
 // from global memory by buffer loads into LDS (lane l writes slot l of a 1 KB
 // run; rows past the item's last key are out of the buffer's range and read
 // as zero).
@@ -73,8 +78,10 @@ struct AttnTileShape {
   static constexpr int PER_WAVE = INSTS / 4;
 };
 
-template <int D, int G>
-__global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
+// RB: 16-row blocks per wave (a block's item holds 64 RB (query, head) rows);
+// with RB = 1 two blocks share a CU.
+template <int D, int G, int RB>
+__global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
   using S = AttnTileShape<D>;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
@@ -93,19 +100,29 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   // loads: instruction m of this wave covers rows r0 + m * 4 * ROWS_PER_INST
   const int r0 = wave * S::ROWS_PER_INST + lane / S::CH;
   const int cpos = lane % S::CH;
-  const uint32_t kslot = (uint32_t)((cpos ^ (r0 & 7)) * 16);          // (r0 + 4k*RPI) & 7 == r0 & 7
-  const uint32_t vslot = (uint32_t)((cpos ^ ((r0 & 3) << 1)) * 16);
-  // K operand reads: row kb*16 + l16, chunk (s*4 + lg) ^ (l16 & 7)
-  const int xb = (l16 >> 2) & 1, xl = l16 & 3;
-  const int kbase_even = l16 * S::ROW_BYTES + 64 * xb + 16 * (lg ^ xl);
-  const int kbase_odd = l16 * S::ROW_BYTES - 64 * xb + 16 * (lg ^ xl);
-  // V^T operand (transposing reads): row t2*32 + hlf*16 + lg*4 + (l16 >> 2),
-  // dims db*16 + (l16 & 3)*4 .. +4, chunk 2 (db ^ z) + b with z = (l16 >> 2) & 3
-  const int z = (l16 >> 2) & 3;
-  int vbase[4];
+  // instruction m covers rows r0 + 4 m RPI: (r0 + 4 m RPI) % 8 == r0 % 8, and
+  // % 16 alternates with m when 4 RPI == 8
+  uint32_t kslot[2], vslot;
+  kslot[0] = (uint32_t)((cpos ^ (r0 & 15)) * 16);
+  kslot[1] = (uint32_t)((cpos ^ ((r0 + 4 * S::ROWS_PER_INST) & 15)) * 16);
+  vslot = (uint32_t)((cpos ^ ((r0 & 7) << 1)) * 16);
+  // K operand reads: row kb*16 + l16, chunk (s*4 + lg) ^ l16
+  //   = 4 ((s & ~3) | ((s & 3) ^ (l16 >> 2))) + (lg ^ (l16 & 3))
+  int kbase[4];
 #pragma unroll
-  for (int dl = 0; dl < 4; ++dl)
-    vbase[dl] = (lg * 4 + (l16 >> 2)) * S::ROW_BYTES + 32 * (dl ^ z) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
+  for (int s4 = 0; s4 < 4; ++s4)
+    kbase[s4] = l16 * S::ROW_BYTES + 64 * (s4 ^ (l16 >> 2)) + 16 * (lg ^ (l16 & 3));
+  // V^T operand (transposing reads): row t2*32 + hlf*16 + lg*4 + (l16 >> 2),
+  // dims db*16 + (l16 & 3)*4 .. +4: 32-byte pair (db ^ zz) with zz = row % 8
+  const int zz = ((lg & 1) << 2) | (l16 >> 2);
+  int vbase[8];
+#pragma unroll
+  for (int dl = 0; dl < 8; ++dl)
+    vbase[dl] = (lg * 4 + (l16 >> 2)) * S::ROW_BYTES + 32 * (dl ^ zz) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
+
+  // LDS: K tiles in buffers 0/1, V tiles in buffers 2/3
+  unsigned char* const kbuf[2] = {smem_attn, smem_attn + S::TILE_BYTES};
+  unsigned char* const vbuf[2] = {smem_attn + 2 * S::TILE_BYTES, smem_attn + 3 * S::TILE_BYTES};
 
   while (probe < 8) {
     const int x = (home + probe) & 7;
@@ -142,35 +159,33 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       entry0 = (int64_t)a.rev_indptr[h * a.C + c] + qb;
     }
     if (nkeys <= 0) continue;
+    const int ntiles = (nkeys + KT - 1) / KT;
     const uint32_t rs_bytes = (uint32_t)(rs * 2);
     const uint32_t kvoff = (uint32_t)r0 * rs_bytes;
 
-    // direct loads of tile t0 into buffer `buf`
-    auto issue_tile = [&](int t0, int buf) {
-      const uint32_t valid = (uint32_t)(nkeys - t0) * rs_bytes;   // rows past the item read 0
-      __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(kp + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
-      __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(vp + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
-      unsigned char* kdst = smem_attn + buf * S::BUF_BYTES + wave * 1024;
-      unsigned char* vdst = kdst + S::TILE_BYTES;
+    // direct loads of the K (or V) rows of tile t into an LDS buffer; rows
+    // past the item's last key are outside the buffer range and read as 0
+    auto issue = [&](const bf16_t* base, int t, unsigned char* dst_tile, bool is_k) {
+      const int t0 = t * KT;
+      const uint32_t valid = (uint32_t)(nkeys - t0) * rs_bytes;
+      __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(base + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
+      unsigned char* dst = dst_tile + wave * 1024;
 #pragma unroll
       for (int m = 0; m < S::PER_WAVE; ++m) {
         const uint32_t roff = kvoff + (uint32_t)(m * 4 * S::ROWS_PER_INST) * rs_bytes;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(kdst + m * 4096), 16, roff + kslot, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(vdst + m * 4096), 16, roff + vslot, 0, 0, 0);
+        const uint32_t slot = is_k ? kslot[m & 1] : vslot;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst + m * 4096), 16, roff + slot, 0, 0, 0);
       }
     };
 
-    issue_tile(0, 0);   // in flight while the queries load
-
-    // Q rows of this wave: R = wave*32 + rb*16 + l16 -> (slot i, head j)
-    u32x4_t qr[2][KS];
-    int qlim[2];
-    int qidx_r[2];
+    // Q rows of this wave: R = wave*16*RB + rb*16 + l16 -> (slot i, head j)
+    u32x4_t qr[RB][KS];
+    int qlim[RB];
+    int qidx_r[RB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int R = wave * 32 + rb * 16 + l16;
+    for (int rb = 0; rb < RB; ++rb) {
+      const int R = wave * 16 * RB + rb * 16 + l16;
       const int i = R / G, j = R % G;
       const bool ok = i < qn;
       int qidx = 0;
@@ -183,145 +198,250 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         qr[rb][s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
     }
     // the last key any row of this wave may see, and the last key every row sees
-    int wave_lim = max(qlim[0], qlim[1]);
-    int wave_min = min(qidx_r[0] >= 0 ? qlim[0] : 0x7fffffff, qidx_r[1] >= 0 ? qlim[1] : 0x7fffffff);
+    int wave_lim = qlim[0], wave_min = 0x7fffffff;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      wave_lim = max(wave_lim, qlim[rb]);
+      if (qidx_r[rb] >= 0) wave_min = min(wave_min, qlim[rb]);
+    }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
       wave_min = min(wave_min, __shfl_xor(wave_min, o, 64));
     }
 
-    f32x4_t o[DB][2];
+    // S^T = K Q^T for one tile: lane holds keys kb*16 + lg*4 + i of row (rb, l16).
+    // K fragments (s, kb) are read KA_AHEAD ahead of their MFMAs.
+    constexpr int NKF = KS * KB;
+    constexpr int KA_AHEAD = 3;
+    auto kread = [&](const unsigned char* sK, int f) -> u32x4_t {
+      const int s = f / KB, kb = f % KB;
+      const unsigned char* kb0 = sK + kbase[s & 3] + 256 * (s >> 2);
+      return *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * S::ROW_BYTES);
+    };
+    auto gemm_s_body = [&](f32x4_t (&sacc)[KB][RB], const unsigned char* sK) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      o[db][0] = f32x4_t{0, 0, 0, 0};
-      o[db][1] = f32x4_t{0, 0, 0, 0};
-    }
-    float m_run[2] = {NEG_INF, NEG_INF};
-    float l_run[2] = {0.f, 0.f};
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) sacc[kb][rb] = f32x4_t{0, 0, 0, 0};
+      u32x4_t ka[KA_AHEAD];
+#pragma unroll
+      for (int f = 0; f < KA_AHEAD; ++f) ka[f] = kread(sK, f);
+#pragma unroll
+      for (int f = 0; f < NKF; ++f) {
+        const u32x4_t cur = ka[f % KA_AHEAD];
+        if (f + KA_AHEAD < NKF) ka[f % KA_AHEAD] = kread(sK, f + KA_AHEAD);
+        const int s = f / KB, kb = f % KB;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sacc[kb][rb] = mfma16x16x32(as_bf16x8(cur), as_bf16x8(qr[rb][s]), sacc[kb][rb]);
+      }
+    };
+    auto gemm_s = [&](f32x4_t (&sacc)[KB][RB], const unsigned char* sK) {
+      gemm_s_body(sacc, sK);
+      __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
+#pragma unroll
+      for (int f = 0; f < NKF - KA_AHEAD; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RB * KA_AHEAD, 0);
+    };
 
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    int cur = 0;
-    for (int t0 = 0; t0 < nkeys; t0 += KT) {
-      const bool more = t0 + KT < nkeys;
-      if (more) issue_tile(t0 + KT, cur ^ 1);   // streams in during these MFMAs
-      const unsigned char* sK = smem_attn + cur * S::BUF_BYTES;
-      const unsigned char* sV = sK + S::TILE_BYTES;
-
-      if (t0 <= wave_lim) {
-        // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of row (rb, l16)
-        f32x4_t sacc[4][2];
+    // masking of tile t (only tiles that cross the item's end or a row's
+    // causal limit) and this lane's running maximum of the raw scores
+    float lmax_all[RB];
+    auto mask_track = [&](f32x4_t (&sacc)[KB][RB], int t) {
+      const int t0 = t * KT;
+      if (t0 + KT > nkeys || t0 + KT - 1 > wave_min) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          sacc[kb][0] = f32x4_t{0, 0, 0, 0};
-          sacc[kb][1] = f32x4_t{0, 0, 0, 0};
-        }
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const unsigned char* kb0 = sK + ((s & 1) ? kbase_odd : kbase_even) + 64 * s;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * S::ROW_BYTES);
-            sacc[kb][0] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[0][s]), sacc[kb][0]);
-            sacc[kb][1] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[1][s]), sacc[kb][1]);
-          }
-        }
-
-        // online softmax in the log2 domain, with a lazily raised maximum;
-        // only tiles that cross the item's end or a row's causal limit are masked
-        if (t0 + KT > nkeys || t0 + KT - 1 > wave_min) {
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const int key = t0 + kb * 16 + lg * 4 + i;
-                if (!(key < nkeys && key <= qlim[rb])) sacc[kb][rb][i] = NEG_INF;
-              }
-        }
-        u32x4_t pb[2][2];
-        float alpha[2];
-        bool need_any = false;
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          float mx = NEG_INF;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kb][rb][i]);
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          mx *= a.scale_log2;                      // scale > 0: the maximum commutes
-          const bool raise = mx > m_run[rb] + RESCALE_LOG2 || (m_run[rb] == NEG_INF && mx != NEG_INF);
-          const float m_new = raise ? mx : m_run[rb];
-          const float m_use = (m_new == NEG_INF) ? 0.f : m_new;
-          alpha[rb] = raise ? exp2f(m_run[rb] - m_use) : 1.0f;
-          need_any |= raise;
-          float sum = 0.f;
-#pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
+          for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rb][i], a.scale_log2, -m_use));
-              sacc[kb][rb][i] = p;
-              sum += p;
+              const int key = t0 + kb * 16 + lg * 4 + i;
+              if (!(key < nkeys && key <= qlim[rb])) sacc[kb][rb][i] = NEG_INF;
             }
-          sum += __shfl_xor(sum, 16, 64);
-          sum += __shfl_xor(sum, 32, 64);
-          l_run[rb] = l_run[rb] * alpha[rb] + sum;
-          m_run[rb] = m_new;
+      }
 #pragma unroll
-          for (int t2 = 0; t2 < 2; ++t2) {
-            pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
-            pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
-            pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
-            pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
-          }
-        }
-        if (__ballot(need_any)) {
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            o[db][0] *= alpha[0];
-            o[db][1] *= alpha[1];
-          }
-        }
+        for (int kb = 0; kb < KB; ++kb)
+          lmax_all[rb] = fmaxf(lmax_all[rb], fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]),
+                                                   fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
+    };
 
-        // O^T += V^T P^T; transposing LDS reads: lane i of a 16-lane group reads
-        // row K0 + i/4, dims 4 (i%4).. of a d-block and receives dim (block + i)
-        // of rows K0..K0+3.
+    // probabilities exp2(s - m) of tile t against the row's reference maximum,
+    // as the B operand of O^T += V^T P^T: keys {t2*32 + 4 lg..+3,
+    // t2*32 + 16 + 4 lg..+3} of row (rb, l16)
+    float m_ref[RB], l_part[RB];
+    auto exp_pack = [&](f32x4_t (&sacc)[KB][RB], u32x4_t (&pb)[RB][T2]) {
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
+      for (int rb = 0; rb < RB; ++rb) {
+        float sum = 0.f;
 #pragma unroll
-          for (int t2 = 0; t2 < 2; ++t2) {
-            s16x4_t part[2];
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int hlf = 0; hlf < 2; ++hlf) {
-              const unsigned char* p = sV + vbase[db & 3] + (t2 * 32 + hlf * 16) * S::ROW_BYTES + 128 * (db >> 2);
-              part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
-            }
-            u32x4_t va;
-            __builtin_memcpy(&va, part, 16);
-            o[db][0] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[0][t2]), o[db][0]);
-            o[db][1] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb[1][t2]), o[db][1]);
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rb][i], a.scale_log2, -m_ref[rb]));
+            sacc[kb][rb][i] = p;
+            sum += p;
           }
+        l_part[rb] += sum;
+#pragma unroll
+        for (int t2 = 0; t2 < T2; ++t2) {
+          pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
+          pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
+          pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
+          pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
         }
+      }
+    };
+
+    // O^T += V^T P^T; transposing LDS reads: lane i of a 16-lane group reads
+    // row K0 + i/4, dims 4 (i%4).. of a d-block and receives dim (block + i)
+    // of rows K0..K0+3.  The reads run VA_AHEAD fragments ahead of the MFMAs.
+    f32x4_t o[DB][RB];
+    auto gemm_pv = [&](const u32x4_t (&pb)[RB][T2], const unsigned char* sV) {
+      constexpr int NF = DB * T2;         // fragments (db, t2)
+      constexpr int VA_AHEAD = 4;
+      u32x4_t va[VA_AHEAD];
+      auto vread = [&](int f) -> u32x4_t {
+        const int db = f / T2, t2 = f % T2;
+        s16x4_t part[2];
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf) {
+          const unsigned char* p = sV + vbase[db & 7] + (t2 * 32 + hlf * 16) * S::ROW_BYTES + 256 * (db >> 3);
+          part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+        }
+        u32x4_t r;
+        __builtin_memcpy(&r, part, 16);
+        return r;
+      };
+#pragma unroll
+      for (int f = 0; f < VA_AHEAD; ++f) va[f] = vread(f);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const u32x4_t cur = va[f % VA_AHEAD];
+        if (f + VA_AHEAD < NF) va[f % VA_AHEAD] = vread(f + VA_AHEAD);
+        const int db = f / T2, t2 = f % T2;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          o[db][rb] = mfma16x16x32(as_bf16x8(cur), as_bf16x8(pb[rb][t2]), o[db][rb]);
+      }
+      // keep VA_AHEAD fragments of reads in flight ahead of the MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VA_AHEAD, 0);
+#pragma unroll
+      for (int f = 0; f < NF - VA_AHEAD; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RB * VA_AHEAD, 0);
+    };
+
+    // One step: S(t+1) on the MFMA units while the VALU turns S(t) into
+    // probabilities, then O += V(t) P(t).  K(t+2) and V(t+1) stream into the
+    // buffers that K(t) and V(t-1) left.
+    auto step = [&](int t, f32x4_t (&cur)[KB][RB], f32x4_t (&nxt)[KB][RB]) {
+      if (t + 2 < ntiles) issue(kp, t + 2, kbuf[t & 1], true);
+      if (t + 1 < ntiles) issue(vp, t + 1, vbuf[(t + 1) & 1], false);
+      const bool act = t * KT <= wave_lim;
+      const bool act_n = t + 1 < ntiles && (t + 1) * KT <= wave_lim;
+      u32x4_t pb[RB][T2];
+      if (act) mask_track(cur, t);
+      if (act && act_n) {
+        gemm_s_body(nxt, kbuf[(t + 1) & 1]);
+        exp_pack(cur, pb);
+        // the VALU work of exp_pack between the MFMAs of S(t+1)
+        __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
+#pragma unroll
+        for (int f = 0; f < NKF - KA_AHEAD; ++f) {
+          __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2 * RB, 0);
+        }
+#pragma unroll
+        for (int f = 0; f < KA_AHEAD; ++f) {
+          __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2 * RB, 0);
+        }
+      } else if (act) {
+        exp_pack(cur, pb);
+      } else if (act_n) {
+        gemm_s(nxt, kbuf[(t + 1) & 1]);
+      }
+      if (act) gemm_pv(pb, vbuf[t & 1]);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    };
+
+    // Each row's probabilities are taken against a reference maximum fixed
+    // from the first tile; no accumulator is rescaled in the loop.  A key
+    // more than OVERFLOW_LOG2 above the reference (probabilities past 2^64)
+    // restarts the item with the rows' true maxima as reference.
+    bool forced = false;
+    for (int pass = 0; pass < 2; ++pass) {
+      issue(kp, 0, kbuf[0], true);
+      issue(vp, 0, vbuf[0], false);
+      if (ntiles > 1) issue(kp, 1, kbuf[1], true);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) o[db][rb] = f32x4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        l_part[rb] = 0.f;
+        lmax_all[rb] = NEG_INF;
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      cur ^= 1;
+      f32x4_t sA[KB][RB], sB[KB][RB];
+      gemm_s(sA, kbuf[0]);
+      mask_track(sA, 0);
+      if (!forced) {
+        // reference maximum: the row's maximum over the first tile (key 0 of
+        // an item is visible to every row, so it is finite)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          float mx = lmax_all[rb];
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          m_ref[rb] = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
+        }
+      }
+      for (int t = 0; t < ntiles; t += 2) {
+        step(t, sA, sB);
+        if (t + 1 < ntiles) step(t + 1, sB, sA);
+      }
+      // the rows' true maxima; restart if any exceeds its reference by too much
+      bool over = false;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        float mx = lmax_all[rb];
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
+        over |= mx > m_ref[rb] + OVERFLOW_LOG2;
+        if (!forced) lmax_all[rb] = mx;     // kept for a second pass
+      }
+      if (forced || !__syncthreads_or(over ? 1 : 0)) break;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) m_ref[rb] = lmax_all[rb];
+      forced = true;
     }
 
     // epilogue: normalise, write the partial (or the local window) and its LSE
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int R = wave * 32 + rb * 16 + l16;
+    for (int rb = 0; rb < RB; ++rb) {
+      float l = l_part[rb];
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      const int R = wave * 16 * RB + rb * 16 + l16;
       const int i = R / G, j = R % G;
       if (qidx_r[rb] < 0) continue;
-      const float l = l_run[rb];
       const float inv = (l > 0.f) ? 1.0f / l : 0.f;
-      const float lse = (l > 0.f) ? (m_run[rb] + log2f(l)) * 0.69314718055994531f : NEG_INF;
+      const float lse = (l > 0.f) ? (m_ref[rb] + log2f(l)) * 0.69314718055994531f : NEG_INF;
       bf16_t* dst;
       float* ldst;
       if (local) {
@@ -406,11 +526,23 @@ int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
   const size_t lds = AttnTileShape<D>::LDS_BYTES;
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)attn_items_kernel<D, G>,
+    hipFuncSetAttribute((const void*)attn_items_kernel<D, G, PREFILL_RB>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
-  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), lds, stream, a);
+  static int auto_grid = 0;
+  if (grid <= 0) {
+    if (!auto_grid) {
+      int dev = 0, cus = 0, occ = 0;
+      hipGetDevice(&dev);
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)attn_items_kernel<D, G, PREFILL_RB>,
+                                                   256, lds);
+      auto_grid = (cus > 0 ? cus : 256) * (occ > 0 ? occ : 1);
+    }
+    grid = auto_grid;
+  }
+  hipLaunchKernelGGL((attn_items_kernel<D, G, PREFILL_RB>), dim3(grid), dim3(256), lds, stream, a);
   return SBSA_OK;
 }
 
@@ -457,6 +589,8 @@ int combine_dispatch(int D, int G, const int32_t* qmask, const int32_t* nvis,
 
 extern "C" {
 
+int sbsa_prefill_item_rows(void) { return PREFILL_ROWS; }
+
 int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queries,
                         int num_q_heads, int num_kv_heads, int dim, const void* packed,
                         int64_t packed_len, const void* k_orig, const void* v_orig, int64_t o_st,
@@ -498,7 +632,6 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   a.chunk_start = chunk_start;
   a.wstart = wstart;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  if (grid < 1) grid = 512;
   int rc = attn_dispatch(dim, num_q_heads / num_kv_heads, a, grid, stream);
   if (rc) return rc;
   SBSA_CHECK_LAUNCH();

@@ -22,16 +22,9 @@ import torch
 
 from . import _lib
 
-ROWS_PER_ITEM = 128
-
-
 def queries_per_item(q_per_kv: int) -> int:
-    return ROWS_PER_ITEM // q_per_kv
-
-
-def default_grid(device: torch.device) -> int:
-    props = torch.cuda.get_device_properties(device)
-    return int(props.multi_processor_count)
+    """Queries of one work item: the kernel's (query, head) rows per item over G."""
+    return _lib.query("sbsa_prefill_item_rows") // q_per_kv
 
 
 def build_reverse_index(qmask: torch.Tensor, live: torch.Tensor, *, num_queries: int,
@@ -116,7 +109,7 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
               _lib.ptr(rev_indptr), _lib.ptr(qvals), _lib.ptr(items), _lib.ptr(queue),
               _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
               local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), int(chunk_start),
-              int(wstart), float(sm_scale), int(grid or default_grid(dev)), s)
+              int(wstart), float(sm_scale), int(grid or 0), s)
     if timing is not None:
         timing.end(s)
     if out is None:
@@ -160,7 +153,7 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
               None, 0, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), None, None, 32, None,
               None, _lib.ptr(items), _lib.ptr(queue), None, None,
               _lib.ptr(out), out.stride(0), out.stride(1), None, int(chunk_start), 0,
-              float(sm_scale), int(grid or default_grid(dev)), s)
+              float(sm_scale), int(grid or 0), s)
     if timing is not None:
         timing.end(s)
     return out
