@@ -27,6 +27,9 @@ FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed fp32 arithmetic is disabled for every HIP object
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs (gfx950 MFMAs read and write either file): no
+    # AGPR copies around the VALU work on the S tiles
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I", str(HERE.parent / "include"),
     "-Wno-unused-result",
 ]

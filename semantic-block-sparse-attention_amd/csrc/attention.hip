@@ -44,52 +44,65 @@ struct AttnArgs {
   float scale_log2;         // sm_scale * log2(e)
 };
 
-constexpr int KT = 32;      // keys per tile
-constexpr int PREFILL_RB = 2;                       // 16-row blocks per wave
-constexpr int PREFILL_ROWS = 4 * 16 * PREFILL_RB;   // (query, head) rows per work item
-constexpr int KB = KT / 16; // 16-key blocks per tile
-constexpr int T2 = KT / 32; // 32-key MFMA steps of O^T += V^T P^T per tile
+constexpr int KT = 32;                  // keys per tile
+constexpr int PREFILL_ROWS = 128;       // (query, head) rows per work item: 32 per wave
 // Probabilities are taken against a reference maximum per row and may reach
 // 2^OVERFLOW_LOG2 (well inside fp32 and bf16 range) before an item is redone.
 constexpr float OVERFLOW_LOG2 = 64.0f;
 constexpr int BUFFER_CONFIG = 0x00020000;   // raw buffer resource, 32-bit data format
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
-// LDS tile layout: K and V rows of D bf16, row-major; the 16-byte chunks of
-// row r are permuted by an XOR (K: chunk ^ (r % 16), V: chunk ^ 2 (r % 8)) so
-// that the MFMA operand reads of one LDS cycle (16 lanes of 16 bytes for K,
-// 32 lanes of 8 bytes for the transposing V reads: 256 bytes, the 64 banks)
-// hit distinct banks.  Tiles are filled straight
-// from global memory by buffer loads into LDS (lane l writes slot l of a 1 KB
-// run; rows past the item's last key are out of the buffer's range and read
-// as zero).
+__device__ __forceinline__ const bf16_t* uniform_ptr(const bf16_t* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const bf16_t*)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// LDS tile layout: K and V rows of D bf16, row-major, 16-byte chunks of row r
+// permuted by an XOR so that the operand reads of one LDS cycle (256 bytes,
+// the 64 banks) hit distinct banks:
+//   K: chunk ^ (r % 16)     16 lanes read 16 bytes of 16 different rows
+//   V: chunk ^ 4 (r % 4)    32 lanes read 8 bytes of 4 rows, 64 bytes each
+// Tiles are filled straight from global memory by buffer loads into LDS
+// (lane l writes slot l of a 1 KB run; rows past the item's last key are
+// outside the buffer's range and read as zero).
 template <int D>
 struct AttnTileShape {
   static constexpr int CH = D / 8;                    // 16-byte chunks per row
   static constexpr int ROW_BYTES = D * 2;
   static constexpr int TILE_BYTES = KT * ROW_BYTES;   // one of K or V
-  static constexpr int BUF_BYTES = 2 * TILE_BYTES;    // K then V
-  static constexpr size_t LDS_BYTES = 2 * (size_t)BUF_BYTES;
+  static constexpr size_t LDS_BYTES = 4 * (size_t)TILE_BYTES;   // K, K, V, V
   static constexpr int ROWS_PER_INST = 64 / CH;       // rows one wave instruction covers
   static constexpr int INSTS = KT / ROWS_PER_INST;    // instructions per K (or V) tile
   static constexpr int PER_WAVE = INSTS / 4;
 };
 
-// RB: 16-row blocks per wave (a block's item holds 64 RB (query, head) rows);
-// with RB = 1 two blocks share a CU.
-template <int D, int G, int RB>
-__global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
+// Both GEMMs on bf16 MFMA 32x32x16 in the transposed form: S^T = K Q^T
+// (32 keys x 32 rows per tile) and O^T += V^T P^T (32 dims x 32 rows).  Lane
+// l holds row l % 32 of the wave's 32 (query, head) rows; in S^T it holds keys
+// 8 (i / 4) + 4 (l / 32) + i % 4, i < 16, which are exactly the B operand
+// P^T of the two 16-key steps of O^T (keys {0-3, 8-11 | 4-7, 12-15} and
+// {16-19, 24-27 | 20-23, 28-31}), so the probabilities never leave the lane.
+template <int D, int G>
+__global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   using S = AttnTileShape<D>;
-  constexpr int KS = D / 32;
-  constexpr int DB = D / 16;
+  constexpr int KS = D / 16;        // 16-dim steps of S^T
+  constexpr int DT = D / 32;        // 32-dim tiles of O^T
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
   __shared__ int s_item;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15, lg = lane >> 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar LDS bases
+  const int l32 = lane & 31, g = lane >> 5;
   const float NEG_INF = -INFINITY;
   // blocks are dispatched round-robin over the 8 XCDs: take work from this
   // XCD's queue, then steal from the others
@@ -97,28 +110,29 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
   int probe = 0;
 
   // --- per-lane address bases (fixed for the kernel) ---------------------
-  // loads: instruction m of this wave covers rows r0 + m * 4 * ROWS_PER_INST
+  // loads: instruction m of this wave covers rows r0 + 4 m RPI; their row % 4
+  // is r0 % 4, their row % 16 alternates with m when 4 RPI == 8
   const int r0 = wave * S::ROWS_PER_INST + lane / S::CH;
   const int cpos = lane % S::CH;
-  // instruction m covers rows r0 + 4 m RPI: (r0 + 4 m RPI) % 8 == r0 % 8, and
-  // % 16 alternates with m when 4 RPI == 8
   uint32_t kslot[2], vslot;
   kslot[0] = (uint32_t)((cpos ^ (r0 & 15)) * 16);
   kslot[1] = (uint32_t)((cpos ^ ((r0 + 4 * S::ROWS_PER_INST) & 15)) * 16);
-  vslot = (uint32_t)((cpos ^ ((r0 & 7) << 1)) * 16);
-  // K operand reads: row kb*16 + l16, chunk (s*4 + lg) ^ l16
-  //   = 4 ((s & ~3) | ((s & 3) ^ (l16 >> 2))) + (lg ^ (l16 & 3))
-  int kbase[4];
+  vslot = (uint32_t)((cpos ^ ((r0 & 3) << 2)) * 16);
+  // K operand (A of S^T): row l32, chunk (2 s + g) ^ (l32 % 16); for s < 8 the
+  // chunk stays below 16, past it the XOR keeps the +16 (256 bytes)
+  int kbase[8];
 #pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4)
-    kbase[s4] = l16 * S::ROW_BYTES + 64 * (s4 ^ (l16 >> 2)) + 16 * (lg ^ (l16 & 3));
-  // V^T operand (transposing reads): row t2*32 + hlf*16 + lg*4 + (l16 >> 2),
-  // dims db*16 + (l16 & 3)*4 .. +4: 32-byte pair (db ^ zz) with zz = row % 8
-  const int zz = ((lg & 1) << 2) | (l16 >> 2);
-  int vbase[8];
+  for (int s8 = 0; s8 < 8; ++s8) kbase[s8] = l32 * S::ROW_BYTES + 16 * ((2 * s8 + g) ^ (l32 & 15));
+  // V^T operand (A of O^T, transposing reads): the 16-lane group (g, hh)
+  // covers dims dt*32 + hh*16 .. +16 of rows K0..K0+3 with K0 = 16 m + 4 g
+  // (+8 for the second read); lane i of the group reads row K0 + i/4, dims
+  // 4 (i % 4).., chunk (4 dt + 2 hh + (i % 4)/2) ^ 4 (i / 4)
+  const int i16 = lane & 15, hh = (lane >> 4) & 1;
+  int vbase[4];
 #pragma unroll
-  for (int dl = 0; dl < 8; ++dl)
-    vbase[dl] = (lg * 4 + (l16 >> 2)) * S::ROW_BYTES + 32 * (dl ^ zz) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
+  for (int d4 = 0; d4 < 4; ++d4)
+    vbase[d4] = (4 * g + (i16 >> 2)) * S::ROW_BYTES + 16 * (4 * (d4 ^ (i16 >> 2)) + 2 * hh + ((i16 & 3) >> 1)) +
+                8 * (i16 & 1);
 
   // LDS: K tiles in buffers 0/1, V tiles in buffers 2/3
   unsigned char* const kbuf[2] = {smem_attn, smem_attn + S::TILE_BYTES};
@@ -131,7 +145,7 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
       s_item = v < a.queue[x] ? a.queue[8 + x] + v : -1;
     }
     __syncthreads();
-    const int idx = s_item;
+    const int idx = __builtin_amdgcn_readfirstlane(s_item);   // uniform: scalar loads below
     __syncthreads();
     if (idx < 0) {
       ++probe;
@@ -158,6 +172,12 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
       nkeys = a.nvis[h * a.C + c];
       entry0 = (int64_t)a.rev_indptr[h * a.C + c] + qb;
     }
+    // uniform values (scalar registers): the buffer resources built from them
+    // need no per-lane loop
+    kp = uniform_ptr(kp);
+    vp = uniform_ptr(vp);
+    rs = __builtin_amdgcn_readfirstlane((int)rs);
+    nkeys = __builtin_amdgcn_readfirstlane(nkeys);
     if (nkeys <= 0) continue;
     const int ntiles = (nkeys + KT - 1) / KT;
     const uint32_t rs_bytes = (uint32_t)(rs * 2);
@@ -167,9 +187,9 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
     // past the item's last key are outside the buffer range and read as 0
     auto issue = [&](const bf16_t* base, int t, unsigned char* dst_tile, bool is_k) {
       const int t0 = t * KT;
-      const uint32_t valid = (uint32_t)(nkeys - t0) * rs_bytes;
+      const int valid = __builtin_amdgcn_readfirstlane((int)((uint32_t)(nkeys - t0) * rs_bytes));
       __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(base + (int64_t)t0 * rs), (short)0, (int)valid, BUFFER_CONFIG);
+          (void*)uniform_ptr(base + (int64_t)t0 * rs), (short)0, valid, BUFFER_CONFIG);
       unsigned char* dst = dst_tile + wave * 1024;
 #pragma unroll
       for (int m = 0; m < S::PER_WAVE; ++m) {
@@ -179,142 +199,113 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
       }
     };
 
-    // Q rows of this wave: R = wave*16*RB + rb*16 + l16 -> (slot i, head j)
-    u32x4_t qr[RB][KS];
-    int qlim[RB];
-    int qidx_r[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int R = wave * 16 * RB + rb * 16 + l16;
+    // Q^T (B of S^T): lane holds row R = wave*32 + l32 -> (slot i, head j),
+    // dims 16 s + 8 g .. +8
+    u32x4_t qr[KS];
+    int qidx_r, qlim;
+    {
+      const int R = wave * 32 + l32;
       const int i = R / G, j = R % G;
       const bool ok = i < qn;
       int qidx = 0;
       if (ok) qidx = local ? qb + i : a.qvals[entry0 + i];
-      qidx_r[rb] = ok ? qidx : -1;
-      qlim[rb] = local ? (int)(a.chunk_start + qidx - a.wstart) : 0x7fffffff;
-      const bf16_t* src = a.q + (int64_t)qidx * a.q_sq + (int64_t)(h * G + j) * a.q_sh + lg * 8;
+      qidx_r = ok ? qidx : -1;
+      qlim = local ? (int)(a.chunk_start + qidx - a.wstart) : 0x7fffffff;
+      const bf16_t* src = a.q + (int64_t)qidx * a.q_sq + (int64_t)(h * G + j) * a.q_sh + g * 8;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        qr[rb][s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
+        qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 16) : u32x4_t{0, 0, 0, 0};
     }
     // the last key any row of this wave may see, and the last key every row sees
-    int wave_lim = qlim[0], wave_min = 0x7fffffff;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      wave_lim = max(wave_lim, qlim[rb]);
-      if (qidx_r[rb] >= 0) wave_min = min(wave_min, qlim[rb]);
-    }
+    int wave_lim = qlim, wave_min = qidx_r >= 0 ? qlim : 0x7fffffff;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
       wave_min = min(wave_min, __shfl_xor(wave_min, o, 64));
     }
+    wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
+    wave_min = __builtin_amdgcn_readfirstlane(wave_min);
 
-    // S^T = K Q^T for one tile: lane holds keys kb*16 + lg*4 + i of row (rb, l16).
-    // K fragments (s, kb) are read KA_AHEAD ahead of their MFMAs.
-    constexpr int NKF = KS * KB;
+    // S^T = K Q^T for one tile; K fragments are read KA_AHEAD ahead
     constexpr int KA_AHEAD = 3;
-    auto kread = [&](const unsigned char* sK, int f) -> u32x4_t {
-      const int s = f / KB, kb = f % KB;
-      const unsigned char* kb0 = sK + kbase[s & 3] + 256 * (s >> 2);
-      return *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * S::ROW_BYTES);
+    auto kread = [&](const unsigned char* sK, int s) -> u32x4_t {
+      return *reinterpret_cast<const u32x4_t*>(sK + kbase[s & 7] + 256 * (s >> 3));
     };
-    auto gemm_s_body = [&](f32x4_t (&sacc)[KB][RB], const unsigned char* sK) {
+    auto gemm_s_body = [&](f32x16_t& sacc, const unsigned char* sK) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) sacc[kb][rb] = f32x4_t{0, 0, 0, 0};
+      for (int e = 0; e < 16; ++e) sacc[e] = 0.f;
       u32x4_t ka[KA_AHEAD];
 #pragma unroll
       for (int f = 0; f < KA_AHEAD; ++f) ka[f] = kread(sK, f);
 #pragma unroll
-      for (int f = 0; f < NKF; ++f) {
-        const u32x4_t cur = ka[f % KA_AHEAD];
-        if (f + KA_AHEAD < NKF) ka[f % KA_AHEAD] = kread(sK, f + KA_AHEAD);
-        const int s = f / KB, kb = f % KB;
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          sacc[kb][rb] = mfma16x16x32(as_bf16x8(cur), as_bf16x8(qr[rb][s]), sacc[kb][rb]);
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t cur = ka[s % KA_AHEAD];
+        if (s + KA_AHEAD < KS) ka[s % KA_AHEAD] = kread(sK, s + KA_AHEAD);
+        sacc = mfma32x32x16(as_bf16x8(cur), as_bf16x8(qr[s]), sacc);
       }
     };
-    auto gemm_s = [&](f32x4_t (&sacc)[KB][RB], const unsigned char* sK) {
+    auto gemm_s = [&](f32x16_t& sacc, const unsigned char* sK) {
       gemm_s_body(sacc, sK);
       __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
 #pragma unroll
-      for (int f = 0; f < NKF - KA_AHEAD; ++f) {
-        __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+      for (int f = 0; f < KS - KA_AHEAD; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, RB * KA_AHEAD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, KA_AHEAD, 0);
     };
 
     // masking of tile t (only tiles that cross the item's end or a row's
     // causal limit) and this lane's running maximum of the raw scores
-    float lmax_all[RB];
-    auto mask_track = [&](f32x4_t (&sacc)[KB][RB], int t) {
+    float lmax_all = NEG_INF;
+    auto mask_track = [&](f32x16_t& sacc, int t) {
       const int t0 = t * KT;
       if (t0 + KT > nkeys || t0 + KT - 1 > wave_min) {
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = t0 + kb * 16 + lg * 4 + i;
-              if (!(key < nkeys && key <= qlim[rb])) sacc[kb][rb][i] = NEG_INF;
-            }
-      }
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-          lmax_all[rb] = fmaxf(lmax_all[rb], fmaxf(fmaxf(sacc[kb][rb][0], sacc[kb][rb][1]),
-                                                   fmaxf(sacc[kb][rb][2], sacc[kb][rb][3])));
-    };
-
-    // probabilities exp2(s - m) of tile t against the row's reference maximum,
-    // as the B operand of O^T += V^T P^T: keys {t2*32 + 4 lg..+3,
-    // t2*32 + 16 + 4 lg..+3} of row (rb, l16)
-    float m_ref[RB], l_part[RB];
-    auto exp_pack = [&](f32x4_t (&sacc)[KB][RB], u32x4_t (&pb)[RB][T2]) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        float sum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][rb][i], a.scale_log2, -m_ref[rb]));
-            sacc[kb][rb][i] = p;
-            sum += p;
-          }
-        l_part[rb] += sum;
-#pragma unroll
-        for (int t2 = 0; t2 < T2; ++t2) {
-          pb[rb][t2].x = pack2bf(sacc[2 * t2][rb][0], sacc[2 * t2][rb][1]);
-          pb[rb][t2].y = pack2bf(sacc[2 * t2][rb][2], sacc[2 * t2][rb][3]);
-          pb[rb][t2].z = pack2bf(sacc[2 * t2 + 1][rb][0], sacc[2 * t2 + 1][rb][1]);
-          pb[rb][t2].w = pack2bf(sacc[2 * t2 + 1][rb][2], sacc[2 * t2 + 1][rb][3]);
+        for (int e = 0; e < 16; ++e) {
+          const int key = t0 + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (!(key < nkeys && key <= qlim)) sacc[e] = NEG_INF;
         }
       }
+#pragma unroll
+      for (int e = 0; e < 16; e += 4)
+        lmax_all = fmaxf(lmax_all, fmaxf(fmaxf(sacc[e], sacc[e + 1]), fmaxf(sacc[e + 2], sacc[e + 3])));
     };
 
-    // O^T += V^T P^T; transposing LDS reads: lane i of a 16-lane group reads
-    // row K0 + i/4, dims 4 (i%4).. of a d-block and receives dim (block + i)
-    // of rows K0..K0+3.  The reads run VA_AHEAD fragments ahead of the MFMAs.
-    f32x4_t o[DB][RB];
-    auto gemm_pv = [&](const u32x4_t (&pb)[RB][T2], const unsigned char* sV) {
-      constexpr int NF = DB * T2;         // fragments (db, t2)
+    // probabilities exp2(s - m) of a tile against the row's reference maximum
+    // as the B operands of the two 16-key steps of O^T
+    float m_ref = 0.f, l_part = 0.f;
+    auto exp_pack = [&](f32x16_t& sacc, u32x4_t (&pb)[2]) {
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e], a.scale_log2, -m_ref));
+        sacc[e] = p;
+        sum += p;
+      }
+      l_part += sum;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        pb[m].x = pack2bf(sacc[8 * m + 0], sacc[8 * m + 1]);
+        pb[m].y = pack2bf(sacc[8 * m + 2], sacc[8 * m + 3]);
+        pb[m].z = pack2bf(sacc[8 * m + 4], sacc[8 * m + 5]);
+        pb[m].w = pack2bf(sacc[8 * m + 6], sacc[8 * m + 7]);
+      }
+    };
+
+    // O^T += V^T P^T: two transposing reads per 32-dim x 16-key fragment,
+    // VA_AHEAD fragments ahead of the MFMAs
+    f32x16_t o[DT];
+    auto gemm_pv = [&](const u32x4_t (&pb)[2], const unsigned char* sV) {
+      constexpr int NF = DT * 2;          // fragments (m, dt), m-major
       constexpr int VA_AHEAD = 4;
       u32x4_t va[VA_AHEAD];
       auto vread = [&](int f) -> u32x4_t {
-        const int db = f / T2, t2 = f % T2;
+        const int m = f / DT, dt = f % DT;
+        const unsigned char* p = sV + vbase[dt & 3] + 256 * (dt >> 2) + 16 * m * S::ROW_BYTES;
         s16x4_t part[2];
-#pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf) {
-          const unsigned char* p = sV + vbase[db & 7] + (t2 * 32 + hlf * 16) * S::ROW_BYTES + 256 * (db >> 3);
-          part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
-        }
+        part[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+        part[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(p + 8 * S::ROW_BYTES));
         u32x4_t r;
         __builtin_memcpy(&r, part, 16);
         return r;
@@ -325,30 +316,27 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
       for (int f = 0; f < NF; ++f) {
         const u32x4_t cur = va[f % VA_AHEAD];
         if (f + VA_AHEAD < NF) va[f % VA_AHEAD] = vread(f + VA_AHEAD);
-        const int db = f / T2, t2 = f % T2;
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          o[db][rb] = mfma16x16x32(as_bf16x8(cur), as_bf16x8(pb[rb][t2]), o[db][rb]);
+        const int m = f / DT, dt = f % DT;
+        o[dt] = mfma32x32x16(as_bf16x8(cur), as_bf16x8(pb[m]), o[dt]);
       }
-      // keep VA_AHEAD fragments of reads in flight ahead of the MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * VA_AHEAD, 0);
 #pragma unroll
       for (int f = 0; f < NF - VA_AHEAD; ++f) {
-        __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, RB * VA_AHEAD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, VA_AHEAD, 0);
     };
 
     // One step: S(t+1) on the MFMA units while the VALU turns S(t) into
     // probabilities, then O += V(t) P(t).  K(t+2) and V(t+1) stream into the
     // buffers that K(t) and V(t-1) left.
-    auto step = [&](int t, f32x4_t (&cur)[KB][RB], f32x4_t (&nxt)[KB][RB]) {
+    auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
       if (t + 2 < ntiles) issue(kp, t + 2, kbuf[t & 1], true);
       if (t + 1 < ntiles) issue(vp, t + 1, vbuf[(t + 1) & 1], false);
       const bool act = t * KT <= wave_lim;
       const bool act_n = t + 1 < ntiles && (t + 1) * KT <= wave_lim;
-      u32x4_t pb[RB][T2];
+      u32x4_t pb[2];
       if (act) mask_track(cur, t);
       if (act && act_n) {
         gemm_s_body(nxt, kbuf[(t + 1) & 1]);
@@ -356,15 +344,15 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
         // the VALU work of exp_pack between the MFMAs of S(t+1)
         __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
 #pragma unroll
-        for (int f = 0; f < NKF - KA_AHEAD; ++f) {
-          __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
+        for (int f = 0; f < KS - KA_AHEAD; ++f) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2 * RB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         }
 #pragma unroll
         for (int f = 0; f < KA_AHEAD; ++f) {
-          __builtin_amdgcn_sched_group_barrier(0x008, RB, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2 * RB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         }
       } else if (act) {
         exp_pack(cur, pb);
@@ -386,79 +374,63 @@ __global__ __launch_bounds__(256, 3 - RB) void attn_items_kernel(AttnArgs a) {
       issue(vp, 0, vbuf[0], false);
       if (ntiles > 1) issue(kp, 1, kbuf[1], true);
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) o[db][rb] = f32x4_t{0, 0, 0, 0};
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        l_part[rb] = 0.f;
-        lmax_all[rb] = NEG_INF;
-      }
+        for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+      l_part = 0.f;
+      lmax_all = NEG_INF;
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      f32x4_t sA[KB][RB], sB[KB][RB];
+      f32x16_t sA, sB;
       gemm_s(sA, kbuf[0]);
       mask_track(sA, 0);
       if (!forced) {
         // reference maximum: the row's maximum over the first tile (key 0 of
         // an item is visible to every row, so it is finite)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-          float mx = lmax_all[rb];
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          m_ref[rb] = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
-        }
+        const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
+        m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
       for (int t = 0; t < ntiles; t += 2) {
         step(t, sA, sB);
         if (t + 1 < ntiles) step(t + 1, sB, sA);
       }
-      // the rows' true maxima; restart if any exceeds its reference by too much
-      bool over = false;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        float mx = lmax_all[rb];
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        mx = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
-        over |= mx > m_ref[rb] + OVERFLOW_LOG2;
-        if (!forced) lmax_all[rb] = mx;     // kept for a second pass
-      }
+      // the row's true maximum; restart if any exceeds its reference by too much
+      float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
+      mx = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
+      const bool over = mx > m_ref + OVERFLOW_LOG2;
       if (forced || !__syncthreads_or(over ? 1 : 0)) break;
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) m_ref[rb] = lmax_all[rb];
+      m_ref = mx;
       forced = true;
     }
 
     // epilogue: normalise, write the partial (or the local window) and its LSE
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float l = l_part[rb];
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
-      const int R = wave * 16 * RB + rb * 16 + l16;
+    {
+      const float l = l_part + __shfl_xor(l_part, 32, 64);
+      const int R = wave * 32 + l32;
       const int i = R / G, j = R % G;
-      if (qidx_r[rb] < 0) continue;
-      const float inv = (l > 0.f) ? 1.0f / l : 0.f;
-      const float lse = (l > 0.f) ? (m_ref[rb] + log2f(l)) * 0.69314718055994531f : NEG_INF;
-      bf16_t* dst;
-      float* ldst;
-      if (local) {
-        dst = a.local_o + (int64_t)qidx_r[rb] * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh;
-        ldst = a.local_lse ? a.local_lse + (int64_t)qidx_r[rb] * a.Hq + h * G + j : nullptr;
-      } else {
-        dst = a.part_o + ((entry0 + i) * G + j) * D;
-        ldst = a.part_lse + (entry0 + i) * G + j;
-      }
+      if (qidx_r >= 0) {
+        const float inv = (l > 0.f) ? 1.0f / l : 0.f;
+        const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
+        bf16_t* dst;
+        float* ldst;
+        if (local) {
+          dst = a.local_o + (int64_t)qidx_r * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh;
+          ldst = a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + j : nullptr;
+        } else {
+          dst = a.part_o + ((entry0 + i) * G + j) * D;
+          ldst = a.part_lse + (entry0 + i) * G + j;
+        }
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        u32x2_t w;
-        w.x = pack2bf(o[db][rb][0] * inv, o[db][rb][1] * inv);
-        w.y = pack2bf(o[db][rb][2] * inv, o[db][rb][3] * inv);
-        *reinterpret_cast<u32x2_t*>(dst + db * 16 + lg * 4) = w;
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            u32x2_t w;
+            w.x = pack2bf(o[dt][4 * q4 + 0] * inv, o[dt][4 * q4 + 1] * inv);
+            w.y = pack2bf(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+            *reinterpret_cast<u32x2_t*>(dst + dt * 32 + 8 * q4 + 4 * g) = w;
+          }
+        if (g == 0 && ldst) *ldst = lse;
       }
-      if (lg == 0 && ldst) *ldst = lse;
     }
   }
 }
@@ -526,7 +498,7 @@ int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
   const size_t lds = AttnTileShape<D>::LDS_BYTES;
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)attn_items_kernel<D, G, PREFILL_RB>,
+    hipFuncSetAttribute((const void*)attn_items_kernel<D, G>,
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     configured = true;
   }
@@ -536,13 +508,13 @@ int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
       int dev = 0, cus = 0, occ = 0;
       hipGetDevice(&dev);
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)attn_items_kernel<D, G, PREFILL_RB>,
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)attn_items_kernel<D, G>,
                                                    256, lds);
       auto_grid = (cus > 0 ? cus : 256) * (occ > 0 ? occ : 1);
     }
     grid = auto_grid;
   }
-  hipLaunchKernelGGL((attn_items_kernel<D, G, PREFILL_RB>), dim3(grid), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), lds, stream, a);
   return SBSA_OK;
 }
 
