@@ -55,6 +55,9 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-queries", type=int, default=64)
     ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one plain 1 GiB device copy (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return ap.parse_args()
 
 
@@ -256,6 +259,14 @@ def main():
         gbs = nbytes / (us * 1e-6) / 1e9
         result.update(decode_us=us, decode_bytes=nbytes, decode_gbs=gbs, decode_tokens=rtok)
         _log(f"decode {us:.2f} us/step, {nbytes / 1e6:.1f} MB/step -> {gbs:.0f} GB/s")
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.int16, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        _log("copy calibration: 1 GiB read, 1 GiB written")
+        del src, dst
     cpu = None
     if not args.no_cpu_baseline and args.only in ("all", "prefill"):
         cpu = cpu_baseline(inp, layer, cfg, args.cpu_sample_queries)
