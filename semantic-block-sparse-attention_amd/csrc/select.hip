@@ -275,37 +275,64 @@ __global__ __launch_bounds__(1024) void rev_scan_kernel(const int32_t* __restric
 // Work list of the KV-outer body, one segment per XCD so that the items that
 // read the same K/V (the query tiles of one KV head's window, the query tiles
 // of one cluster) run on one XCD and share its L2.  Items within a segment:
-// local-window items first (longest first), then cluster items.  Item =
-// {head, cluster or -1, first query slot, query count}.  queue = {n[8],
-// off[8], counter[8]}; the counters are zeroed here.
+// local-window items first (longest first), then cluster items in (head,
+// cluster) order.  Item = {head, cluster or -1, first query slot, query
+// count}.  queue = {n[8], off[8], counter[8]}; the counters are zeroed here.
+// One block: per-XCD counts, each source's first item (a scan per XCD), then
+// every wave expands whole sources (a window tile, or the query tiles of one
+// (head, cluster)) with its 64 lanes.
 __device__ __forceinline__ int local_xcd(int h, int tile, int hkv) {
   const int per = hkv >= 8 ? 1 : 8 / hkv;      // XCDs per KV head
   return ((h * per) + (tile % per)) & 7;
 }
 __device__ __forceinline__ int cluster_xcd(int h, int c, int C) { return (h * C + c) & 7; }
 
+struct ItemSource {
+  int x, n, h, c, qb, qn;
+};
+
+__device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, int s, int nloc, int hkv,
+                                                  int C, int Qc, int QT) {
+  ItemSource r;
+  const int nl = nloc * hkv;
+  if (s < nl) {
+    const int k = s / hkv, tile = nloc - 1 - k;
+    r.h = s % hkv;
+    r.c = -1;
+    r.qb = tile * QT;
+    r.qn = min(QT, Qc - r.qb);
+    r.n = 1;
+    r.x = local_xcd(r.h, tile, hkv);
+  } else {
+    const int e = s - nl;
+    r.h = e / C;
+    r.c = e % C;
+    r.qb = 0;
+    r.qn = rev_counts[e];
+    r.n = (r.qn + QT - 1) / QT;
+    r.x = cluster_xcd(r.h, r.c, C);
+  }
+  return r;
+}
+
 __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __restrict__ rev_counts,
                                                            int hkv, int C, int Qc, int QT,
                                                            int has_local, int4* __restrict__ items,
                                                            int32_t* __restrict__ queue,
                                                            int64_t cap) {
+  extern __shared__ int s_first[];     // [nsrc] first item of each source
   __shared__ int cnt[8];
   __shared__ int off[8];
   __shared__ int wsum[16];
   __shared__ int carry;
   const int nloc = has_local ? (Qc + QT - 1) / QT : 0;
-  const int nl = nloc * hkv;
-  const int ncl = hkv * C;
+  const int nsrc = nloc * hkv + hkv * C;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (threadIdx.x < 8) cnt[threadIdx.x] = 0;
   __syncthreads();
-  for (int e = threadIdx.x; e < nl; e += 1024) {
-    const int k = e / hkv, h = e % hkv;
-    atomicAdd(&cnt[local_xcd(h, nloc - 1 - k, hkv)], 1);
-  }
-  for (int e = threadIdx.x; e < ncl; e += 1024) {
-    const int n = (rev_counts[e] + QT - 1) / QT;
-    if (n) atomicAdd(&cnt[cluster_xcd(e / C, e % C, C)], n);
+  for (int s = threadIdx.x; s < nsrc; s += 1024) {
+    const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+    if (si.n) atomicAdd(&cnt[si.x], si.n);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -319,53 +346,35 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
   for (int x = 0; x < 8; ++x) {
     if (threadIdx.x == 0) carry = off[x];
     __syncthreads();
-    // local items of this XCD, in order
-    for (int base = 0; base < nl; base += 1024) {
-      const int e = base + threadIdx.x;
-      int k = 0, h = 0, tile = 0;
-      bool mine = false;
-      if (e < nl) {
-        k = e / hkv;
-        h = e % hkv;
-        tile = nloc - 1 - k;
-        mine = local_xcd(h, tile, hkv) == x;
-      }
-      const int f = mine ? 1 : 0;
-      const int incl = wave_incl_scan(f);
-      if (lane == 63) wsum[wave] = incl;
-      __syncthreads();
-      int o = carry;
-      for (int w = 0; w < wave; ++w) o += wsum[w];
-      if (mine) {
-        const int pos = o + incl - 1;
-        const int qb = tile * QT;
-        if (pos < cap) items[pos] = make_int4(h, -1, qb, min(QT, Qc - qb));
-      }
-      __syncthreads();
-      if (threadIdx.x == 1023) carry = o + incl;
-      __syncthreads();
-    }
-    // cluster items of this XCD, in (head, cluster) order
-    for (int base = 0; base < ncl; base += 1024) {
-      const int e = base + threadIdx.x;
-      int n = 0, cntq = 0;
-      if (e < ncl && cluster_xcd(e / C, e % C, C) == x) {
-        cntq = rev_counts[e];
-        n = (cntq + QT - 1) / QT;
+    for (int base = 0; base < nsrc; base += 1024) {
+      const int s = base + threadIdx.x;
+      int n = 0;
+      if (s < nsrc) {
+        const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+        if (si.x == x) n = si.n;
       }
       const int incl = wave_incl_scan(n);
       if (lane == 63) wsum[wave] = incl;
       __syncthreads();
       int o = carry;
       for (int w = 0; w < wave; ++w) o += wsum[w];
-      const int first = o + incl - n;
-      for (int j = 0; j < n; ++j) {
-        const int qb = j * QT;
-        if (first + j < cap) items[first + j] = make_int4(e / C, e % C, qb, min(QT, cntq - qb));
-      }
+      if (n) s_first[s] = o + incl - n;
       __syncthreads();
       if (threadIdx.x == 1023) carry = o + incl;
       __syncthreads();
+    }
+  }
+  // expansion: one wave per source
+  for (int s = wave; s < nsrc; s += 16) {
+    const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+    if (!si.n) continue;
+    const int f0 = s_first[s];
+    for (int j = lane; j < si.n; j += 64) {
+      const int64_t pos = (int64_t)f0 + j;
+      if (pos >= cap) break;
+      const int qb = si.c >= 0 ? j * QT : si.qb;
+      const int qn = si.c >= 0 ? min(QT, si.qn - qb) : si.qn;
+      items[pos] = make_int4(si.h, si.c, qb, qn);
     }
   }
   if (threadIdx.x < 8) {
@@ -494,7 +503,17 @@ int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clus
                        int num_queries, int queries_per_item, int has_local, void* items,
                        int64_t items_cap, int32_t* queue, hipStream_t stream) {
   if (!rev_counts || !items || !queue || queries_per_item < 1) return SBSA_ERR_ARG;
-  hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), 0, stream, rev_counts, num_kv_heads,
+  const int nloc = has_local ? (num_queries + queries_per_item - 1) / queries_per_item : 0;
+  const size_t lds = (size_t)(nloc * num_kv_heads + num_kv_heads * num_clusters) * 4;
+  if (lds > 96 * 1024) return SBSA_ERR_UNSUPPORTED;
+  static size_t configured = 0;
+  if (lds > configured) {
+    if (hipFuncSetAttribute((const void*)build_items_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return SBSA_ERR_UNSUPPORTED;
+    configured = lds;
+  }
+  hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), lds, stream, rev_counts, num_kv_heads,
                      num_clusters, num_queries, queries_per_item, has_local, (int4*)items, queue,
                      items_cap);
   SBSA_CHECK_LAUNCH();
