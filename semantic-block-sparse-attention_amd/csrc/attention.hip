@@ -403,33 +403,47 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       forced = true;
     }
 
-    // epilogue: normalise, write the partial (or the local window) and its LSE
+    // epilogue: normalise, then write the partial (or the local window) and
+    // its LSE.  The rows go through this wave's own 32-row slice of the (now
+    // idle) tile buffers, so that every store is 16 bytes per lane and whole
+    // rows per instruction: the item's rows are contiguous in part_o, and
+    // the G heads of a query are contiguous in the window output.
     {
       const float l = l_part + __shfl_xor(l_part, 32, 64);
       const int R = wave * 32 + l32;
-      const int i = R / G, j = R % G;
-      if (qidx_r >= 0) {
-        const float inv = (l > 0.f) ? 1.0f / l : 0.f;
+      const float inv = (l > 0.f) ? 1.0f / l : 0.f;
+      if (qidx_r >= 0 && g == 0) {
+        const int i = R / G, j = R % G;
         const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
-        bf16_t* dst;
-        float* ldst;
-        if (local) {
-          dst = a.local_o + (int64_t)qidx_r * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh;
-          ldst = a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + j : nullptr;
-        } else {
-          dst = a.part_o + ((entry0 + i) * G + j) * D;
-          ldst = a.part_lse + (entry0 + i) * G + j;
+        float* ldst = local ? (a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + j : nullptr)
+                            : a.part_lse + (entry0 + i) * G + j;
+        if (ldst) *ldst = lse;
+      }
+      // 16-byte chunk c of row r sits at chunk c ^ (r % 32) of the row
+      unsigned char* stage = smem_attn + wave * 32 * S::ROW_BYTES;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          u32x2_t w;
+          w.x = pack2bf(o[dt][4 * q4 + 0] * inv, o[dt][4 * q4 + 1] * inv);
+          w.y = pack2bf(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+          const int c = (4 * dt + q4) ^ (l32 & (S::CH - 1));
+          *reinterpret_cast<u32x2_t*>(stage + l32 * S::ROW_BYTES + 16 * c + 8 * g) = w;
         }
+      // read back whole rows: instruction m covers rows ROWS_PER_INST m ..
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            u32x2_t w;
-            w.x = pack2bf(o[dt][4 * q4 + 0] * inv, o[dt][4 * q4 + 1] * inv);
-            w.y = pack2bf(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
-            *reinterpret_cast<u32x2_t*>(dst + dt * 32 + 8 * q4 + 4 * g) = w;
-          }
-        if (g == 0 && ldst) *ldst = lse;
+      for (int m = 0; m < 32 / S::ROWS_PER_INST; ++m) {
+        const int r = m * S::ROWS_PER_INST + lane / S::CH;
+        const int c = lane % S::CH;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + r * S::ROW_BYTES + 16 * (c ^ (r & (S::CH - 1))));
+        const int RR = wave * 32 + r;
+        const int i = RR / G, j = RR % G;
+        if (i < qn) {
+          bf16_t* dst = local ? a.local_o + (int64_t)(qb + i) * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh
+                              : a.part_o + ((entry0 + i) * G + j) * D;
+          *reinterpret_cast<u32x4_t*>(dst + 8 * c) = v;
+        }
       }
     }
   }
