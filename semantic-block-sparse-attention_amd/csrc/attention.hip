@@ -138,19 +138,30 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   unsigned char* const kbuf[2] = {smem_attn, smem_attn + S::TILE_BYTES};
   unsigned char* const vbuf[2] = {smem_attn + 2 * S::TILE_BYTES, smem_attn + 3 * S::TILE_BYTES};
 
-  while (probe < 8) {
-    const int x = (home + probe) & 7;
+  // Thread 0 claims each item one item ahead: the atomic for the next item is
+  // issued when an item starts and resolved when the next one does, so its
+  // latency hides behind the item's work.
+  int pend = 0;
+  if (threadIdx.x == 0) pend = atomicAdd(&a.queue[16 + home], 1);
+  for (;;) {
     if (threadIdx.x == 0) {
-      const int v = atomicAdd(&a.queue[16 + x], 1);
-      s_item = v < a.queue[x] ? a.queue[8 + x] + v : -1;
+      int claimed = -1;
+      for (;;) {
+        const int x = (home + probe) & 7;
+        if (pend < a.queue[x]) {
+          claimed = a.queue[8 + x] + pend;
+          break;
+        }
+        if (++probe == 8) break;
+        pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
+      }
+      s_item = claimed;
+      if (claimed >= 0) pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
     }
     __syncthreads();
     const int idx = __builtin_amdgcn_readfirstlane(s_item);   // uniform: scalar loads below
     __syncthreads();
-    if (idx < 0) {
-      ++probe;
-      continue;
-    }
+    if (idx < 0) break;
     const int4 it = a.items[idx];
     const int h = it.x, c = it.y, qb = it.z, qn = it.w;
     const bool local = c < 0;
