@@ -211,6 +211,68 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      void* workspace, size_t workspace_bytes, void* out, int64_t out_sh,
                      float* out_lse, int32_t* csr_out, hipStream_t stream);
 
+/* ---- S10: token-order streamed prefill (the store behind the fixed clusters) -----
+ * Nearest cluster of each new key: replaces _nearest_cluster
+ * (semblo/vllm_plugin/suffix_flush.py:154-170) applied to routing_space of the
+ * key router's output, as TokenOuterPrefillSession._append does
+ * (semblo/vllm_plugin/token_outer_prefill.py:339-348).  k [n, Hkv, dim] bf16 at
+ * strides (stride_tok, stride_head): pre-RoPE keys (router_pass 1) or the
+ * router's output (0).  Cosine in fp32 against cat(codebooks[h, 0, c],
+ * codebooks[h, 1, c]); all-zero descriptors are never chosen; the first of
+ * equal maxima wins.  ids [Hkv, n] int32.  dim in {128, 256}, C a multiple
+ * of 64 up to 1024. */
+int sbsa_nearest_cluster(const void* k, int64_t n, int64_t stride_tok, int64_t stride_head,
+                         int num_kv_heads, int dim, int router_pass, const void* codebooks,
+                         int num_clusters, int32_t* ids, hipStream_t stream);
+
+/* Destination rows of a slice's keys: replaces append_rows
+ * (semblo/vllm_plugin/token_outer_prefill.py:66-87).  ids [Hkv, n] (cluster of
+ * each key in position order), indptr [Hkv, C+1], sizes [Hkv, C] (keys
+ * already in each run).  rows[h, i] = indptr[h, c] + sizes[h, c] + (earlier
+ * keys of the slice in c); counts [Hkv, C].  reserve [Hkv, C] (optional):
+ * overflow[h] (optional) gets bit 0 when sizes + counts exceeds it for some
+ * cluster, the test of _append (token_outer_prefill.py:350-352); bit 1 flags
+ * an id outside [0, C) (its row is -1).  Reads only: sizes are not advanced. */
+int sbsa_append_rows(const int32_t* ids, int64_t n, int num_kv_heads, int num_clusters,
+                     const int32_t* indptr, const int32_t* sizes, const int32_t* reserve,
+                     int32_t* rows, int32_t* counts, int32_t* overflow, hipStream_t stream);
+
+/* The writes of _append (semblo/vllm_plugin/token_outer_prefill.py:353-364):
+ * packed[t, rows[h, i], h] = (t ? value : key)[i, h], posting[h, rows[h, i]] =
+ * first_position + i, inverse[h, first_position + i] = rows[h, i];
+ * sizes_before (optional) = sizes, then sizes += counts.  key/value [n, Hkv,
+ * dim] at (stride_tok, stride_head); packed [2, packed_len, Hkv, dim];
+ * posting [Hkv, posting_width]; inverse [Hkv, inverse_len]. */
+int sbsa_append_kv(const void* key, const void* value, int64_t stride_tok, int64_t stride_head,
+                   int64_t n, int num_kv_heads, int dim, const int32_t* rows, int64_t first_position,
+                   void* packed, int64_t packed_len, int32_t* posting, int64_t posting_width,
+                   int32_t* inverse, int64_t inverse_len, int32_t* sizes, const int32_t* counts,
+                   int num_clusters, int32_t* sizes_before, hipStream_t stream);
+
+/* Moves positions 0..n-1 from runs starting at old_indptr to the same offsets
+ * in runs starting at new_indptr: the row moves of _fit_and_pack
+ * (semblo/vllm_plugin/token_outer_prefill.py:284-312) and _repack (:366-392).
+ * old_rows [Hkv, >= n] (row stride old_rows_ld) is each position's row in the
+ * old layout; its cluster is the last b with old_indptr[b] <= row.  key/value
+ * [n, Hkv, dim] hold the keys in position order (the staged prompt at the
+ * fit; sbsa_gather_rows' output at a repack).  Writes inverse [Hkv, >= n]
+ * (row stride inverse_ld; must not overlap old_rows), posting[h, new row] =
+ * position and the packed rows. */
+int sbsa_relayout_runs(const void* key, const void* value, int64_t stride_tok, int64_t stride_head,
+                       int64_t n, int num_kv_heads, int dim, const int32_t* old_rows, int64_t old_rows_ld,
+                       const int32_t* old_indptr, const int32_t* new_indptr, int num_clusters,
+                       void* packed, int64_t packed_len, int32_t* posting, int64_t posting_width,
+                       int32_t* inverse, int64_t inverse_ld, hipStream_t stream);
+
+/* Positions first..first+n-1 back in prompt order through the inverse map:
+ * (t ? value_out : key_out)[i, h] = packed[t, inverse[h, first + i], h].  The
+ * gather of _repack (semblo/vllm_plugin/token_outer_prefill.py:380-383) and of
+ * the dense chunks that follow the fit ("read densely by the fused body through
+ * the inverse permutation", token_outer_prefill.py:155-159). */
+int sbsa_gather_rows(const void* packed, int64_t packed_len, int num_kv_heads, int dim,
+                     const int32_t* inverse, int64_t inverse_ld, int64_t first, int64_t n, void* key_out,
+                     void* value_out, int64_t stride_tok, int64_t stride_head, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

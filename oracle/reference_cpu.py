@@ -24,6 +24,8 @@ reference's results bit for bit:
   S6  LSE combine                  kv_outer.py:370-428
   S7-S9 decode step                fused_decode.py:81-358, 393-521
   S8  LSE merge                    paged_attention.py:50-80
+  S10 token-order append           token_outer_prefill.py:39-87, 260-392,
+                                   suffix_flush.py:154-170
 
 Parity pins (each checked by a test in tests/):
   S0   closed form: unit norm of the bf16 result; reproduces the reference's
@@ -37,6 +39,12 @@ Parity pins (each checked by a test in tests/):
   S4   brute-force transpose of the selection mask.
   S5/S6 fp64 brute force over the explicit key set S(p, h).
   S7-S9 fp64 brute force over the selected rows plus the visible suffix.
+  S10  append_rows: the known answers of the reference's own test
+       (tests/test_token_outer_prefill.py:30-38) and a vectorised sort-based
+       form on random slices; reserved_layout: the reference test's
+       properties (whole pages, at least one page, fits the width, ratio) and
+       a hand-computed case; nearest_cluster: fp64 argmax on random keys
+       (near-ties excluded) and the dead-descriptor rule.
 """
 from __future__ import annotations
 
@@ -506,4 +514,90 @@ def decode_reference(q: torch.Tensor, packed: torch.Tensor, indptr: torch.Tensor
         for t in range(g):
             s = (kk @ q[h * g + t].double()) * sm_scale
             out[h * g + t] = torch.softmax(s, dim=0) @ vv
+    return out
+
+
+# ---------------------------------------------------------------- S10 ---------
+
+def reserved_layout(sizes_ref: torch.Tensor, n_ref: int, total_tokens: int, width: int,
+                    align: int) -> torch.Tensor:
+    """token_outer_prefill.py:39-63: rows reserved per cluster, [Hkv, C] int64.
+
+    Each cluster's expected share of ``total_tokens`` (its fraction of the
+    ``n_ref`` reference keys), rounded up to whole pages of ``align`` rows,
+    never below one page; the pages left in ``width`` are then handed out in
+    the same proportions, rounded down.  Raises when the rounded shares alone
+    do not fit.
+    """
+    align = max(int(align), 1)
+    want = sizes_ref.double() * (float(total_tokens) / float(max(int(n_ref), 1)))
+    pages = torch.ceil(want / align).to(torch.int64).clamp_min(1)
+    rows = pages * align
+    for h in range(rows.shape[0]):
+        left = int(width) - int(rows[h].sum())
+        if left < 0:
+            raise RuntimeError(f"head {h}: the reserved layout needs {int(rows[h].sum())} rows, "
+                               f"the store holds {width}")
+        if left >= align:
+            frac = want[h] / max(float(want[h].sum()), 1.0)
+            rows[h] += torch.floor(frac * (left // align)).to(torch.int64) * align
+    return rows
+
+
+def append_rows(ids: torch.Tensor, indptr: torch.Tensor, sizes: torch.Tensor):
+    """token_outer_prefill.py:66-87, as a scan in position order.
+
+    ids [Hkv, n] (cluster of each new key), indptr [Hkv, C+1], sizes [Hkv, C].
+    A key goes to the row after the last key of its cluster: the run start,
+    plus the keys already there, plus the slice's earlier keys of that
+    cluster.  Returns rows [Hkv, n] int64 and counts [Hkv, C] int64.
+    """
+    hkv, n = ids.shape
+    c = sizes.shape[1]
+    rows = torch.empty(hkv, n, dtype=torch.int64)
+    counts = torch.zeros(hkv, c, dtype=torch.int64)
+    for h in range(hkv):
+        nxt = (indptr[h, :c].to(torch.int64) + sizes[h].to(torch.int64)).tolist()
+        cnt = [0] * c
+        for i, b in enumerate(ids[h].tolist()):
+            rows[h, i] = nxt[b]
+            nxt[b] += 1
+            cnt[b] += 1
+        counts[h] = torch.tensor(cnt, dtype=torch.int64)
+    return rows, counts
+
+
+def nearest_cluster(keys: torch.Tensor, codebooks_h: torch.Tensor, *, router_pass: bool = True,
+                    return_sim: bool = False):
+    """The cluster of each new key in _append (token_outer_prefill.py:339-348).
+
+    keys [n, I] of one KV head: pre-RoPE keys, through the identity key router
+    (routing_normalize_keys) when ``router_pass``.  routing_space
+    (flat_index.py:165-166), then _nearest_cluster (suffix_flush.py:154-170):
+    F.normalize in fp32 against cat(codebooks_h[0], codebooks_h[1]) in fp32,
+    all-zero descriptors at -inf, torch.argmax (first maximum).
+    """
+    product = routing_normalize_keys(keys) if router_pass else keys
+    space = routing_space(product)
+    cents = torch.cat([codebooks_h[0], codebooks_h[1]], dim=-1).float()
+    sim = F.normalize(space.float(), dim=-1) @ cents.t()
+    sim[:, cents.norm(dim=-1) == 0] = -float("inf")
+    ids = sim.argmax(dim=-1)
+    return (ids, sim) if return_sim else ids
+
+
+def relayout_rows(old_rows: torch.Tensor, old_indptr: torch.Tensor,
+                  new_indptr: torch.Tensor) -> torch.Tensor:
+    """The row moves of _fit_and_pack / _repack (token_outer_prefill.py:287-292, 376-379).
+
+    A key at row r of the old layout belongs to the last cluster b with
+    old_indptr[b] <= r and keeps its offset in that cluster's new run.
+    old_rows [Hkv, n]; returns new rows [Hkv, n] int64.
+    """
+    out = torch.empty(old_rows.shape, dtype=torch.int64)
+    for h in range(old_rows.shape[0]):
+        ip = old_indptr[h].to(torch.int64).contiguous()
+        r = old_rows[h].to(torch.int64).contiguous()
+        b = torch.searchsorted(ip, r, right=True) - 1
+        out[h] = r - ip[b] + new_indptr[h].to(torch.int64)[b]
     return out

@@ -46,6 +46,13 @@ SIGNATURES = {
     "sbsa_decode_step": (I32, [P, I64, P, I64, I32, P, P, I64, P, P, P, P, P, I64, P, I64, I32, P, I64,
                                I32, I32, I32, I32, I32, F32, F32, F32, I32, I32, F32, I32, I32, P,
                                SZ, P, I64, P, P, P]),
+    "sbsa_nearest_cluster": (I32, [P, I64, I64, I64, I32, I32, I32, P, I32, P, P]),
+    "sbsa_append_rows": (I32, [P, I64, I32, I32, P, P, P, P, P, P, P]),
+    "sbsa_append_kv": (I32, [P, P, I64, I64, I64, I32, I32, P, I64, P, I64, P, I64, P, I64, P, P,
+                             I32, P, P]),
+    "sbsa_relayout_runs": (I32, [P, P, I64, I64, I64, I32, I32, P, I64, P, P, I32, P, I64, P, I64,
+                                 P, I64, P]),
+    "sbsa_gather_rows": (I32, [P, I64, I32, I32, P, I64, I64, I64, P, P, I64, I64, P]),
 }
 
 ERRORS = {1: "bad argument", 2: "unsupported shape", 3: "kernel launch failed",

@@ -54,13 +54,16 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
                           queries_per_block: int = 32, sm_scale: float, iters: int = 16,
                           fa3_page_size: int = 16, kv_outer_default: bool = True,
                           dense_prefix_x: int = 4, local: int = 0, out: torch.Tensor | None = None,
-                          timing=None, **unused) -> torch.Tensor:
+                          timing=None, window_kv=None, **unused) -> torch.Tensor:
     """Attention of one query chunk [chunk_start, chunk_end] (fused_prefill.py:219-482).
 
     While chunk_start <= dense_prefix_x * K the chunk is dense and causal over
     the whole prefix (fused_prefill.py:259-279); otherwise every cluster's
     rows before wstart = chunk_start are read sparsely, per query, and the
-    chunk's own tokens through the exact causal window.
+    chunk's own tokens through the exact causal window.  ``window_kv`` (k, v),
+    rows wstart..chunk_end in prompt order, replaces the slice of
+    ``index.original_kv`` for that window (the token-order prefill, whose
+    store has no prompt-order copy).
     """
     if not kv_outer_default or not fa3_page_size:
         raise NotImplementedError("only the paper path (FA3 page body, KV-outer) is built")
@@ -69,12 +72,12 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     c = index.num_buckets
     cap = dense_prefix_x * target_tokens
     wstart = 0 if chunk_start <= cap else max(0, chunk_start - local)
-    if index.original_kv is None:
+    if index.original_kv is None and (wstart == 0 or window_kv is None):
         raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
                            "(index.original_kv), which this index no longer holds")
-    k_orig, v_orig = index.original_kv
     hq, d = q_chunk.shape[1], q_chunk.shape[2]
     if wstart == 0:
+        k_orig, v_orig = index.original_kv
         if timing is not None:
             # sum over p in the chunk of (p + 1) keys, every query head, 4 D FLOPs per key
             n = q_count
@@ -100,7 +103,13 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
         g = hq // hkv
         window = q_count * (q_count + 1) // 2
         timing.add_flops(4.0 * d * (g * tokens.to(torch.float64).sum() + hq * window))
-    window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
+    if window_kv is not None:
+        if window_kv[0].shape[0] != chunk_end + 1 - wstart:
+            raise ValueError("window_kv must hold positions wstart..chunk_end")
+        window = window_kv
+    else:
+        k_orig, v_orig = index.original_kv
+        window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
     res, _ = kv_outer_attention(q_chunk, index.packed_kv, qmask, causal_sizes,
                                 index.bucket_indptr, sm_scale=sm_scale, page_size=fa3_page_size,
                                 aligned=True, local_kv=window, chunk_start=chunk_start,

@@ -7,12 +7,15 @@ Mirrors the reference's SembloAttention paths that the operator reaches
   _ingest_prompt_kv        index build, packed K/V                            (model.py:1301-1382)
   _run_product_attention   the query-chunk loop                               (model.py:856-1008)
   _full_graph_decode_step  the decode step over the arena                     (model.py:708-783)
+  begin_token_outer_prefill  a token-order prefill session   (token_outer_prefill.py:127-212)
 
 vLLM's metadata, paged cache and profiling branch are not part of this
 build: the layer keeps its own per-request state, and a call with more than
 one token starts a new request.
 """
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -75,9 +78,45 @@ class SembloAttention:
         index.original_kv = (k_post, v)
         return index
 
+    def begin_token_outer_prefill(self, tokens: int, chunk: int, **kw):
+        """A token-order prefill session of ``tokens`` positions in slices of ``chunk``
+        (the reference's layer.begin_token_outer_prefill, streamed_prefill.py:563-564)."""
+        from .token_outer_prefill import TokenOuterPrefillSession
+        self.index = None
+        self.arena = None
+        return TokenOuterPrefillSession(self, tokens, chunk, **kw)
+
+    def adopt_index(self, index: ProductPostingIndex) -> None:
+        """Make a finished prompt index the layer's decode state."""
+        cfg = self.runtime_config
+        index.original_kv = None
+        self.index = index
+        self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
+                                 suffix_splits=cfg.decode_suffix_splits)
+
+    def prefill_token_order(self, q_post, q_pre, k_pre, k_post, v, output, chunk: int,
+                            timing=None, **kw) -> torch.Tensor:
+        """The whole prompt in token order, one ``chunk``-position slice after another
+        (streamed_prefill.py:547-593 for one layer)."""
+        length = q_post.shape[0]
+        hq, hkv, d = self.num_heads, self.num_kv_heads, self.head_dim
+        session = self.begin_token_outer_prefill(length, chunk, **kw)
+        out = output.view(length, hq, d)
+        for start in range(0, length, chunk):
+            stop = min(length, start + chunk)
+            session.slice(q_post.view(length, hq, d)[start:stop], q_pre.view(length, hq, d)[start:stop],
+                          k_pre.view(length, hkv, d)[start:stop], k_post.view(length, hkv, d)[start:stop],
+                          v.view(length, hkv, d)[start:stop], start, stop, out=out[start:stop],
+                          timing=timing)
+        session.finish()
+        return output
+
     def prefill(self, q_post, q_pre, k_pre, k_post, v, output, timing=None) -> torch.Tensor:
         cfg = self.runtime_config
         length = q_post.shape[0]
+        if os.environ.get("SEMBLO_PREFILL_ORDER", "layer") == "token":
+            chunk = int(os.environ.get("SEMBLO_PREFILL_CHUNK", "0") or 0) or cfg.query_chunk_size
+            return self.prefill_token_order(q_post, q_pre, k_pre, k_post, v, output, chunk, timing=timing)
         q = q_post.view(length, self.num_heads, self.head_dim)
         qp = q_pre.view(length, self.num_heads, self.head_dim)
         kp = k_pre.view(length, self.num_kv_heads, self.head_dim)
@@ -98,9 +137,7 @@ class SembloAttention:
                 temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
                 target_tokens=self.target_tokens, sm_scale=self.scaling, iters=cfg.iters,
                 dense_prefix_x=cfg.dense_prefix_x, out=out[start:end], timing=timing)
-        index.original_kv = None
-        self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
-                                 suffix_splits=cfg.decode_suffix_splits)
+        self.adopt_index(index)
         return output
 
     # -- decode -----------------------------------------------------------------

@@ -1,0 +1,350 @@
+"""Token-order streamed prefill (S10): one slice of the prompt through a layer at a time.
+
+Host side of the reference's semblo/vllm_plugin/token_outer_prefill.py, with
+every array operation on the GPU through libsbsa.  In each sparse layer:
+
+  dense   while a slice starts before the fit point, its K/V are staged in
+          prompt order and it attends exactly over positions 0..p
+          (token_outer_prefill.py:214-255);
+  fit     at the first slice past the fit point, the clusters are fitted on
+          the staged keys with the cluster count the whole prompt would get,
+          and the staged keys move into a store laid out with a reservation
+          per cluster sized from the observed proportions
+          (token_outer_prefill.py:260-337; sbsa_relayout_runs);
+  append  every later slice assigns its keys to the fixed clusters
+          (sbsa_nearest_cluster), appends them behind their cluster's last key
+          (sbsa_append_rows, sbsa_append_kv) and attends through the KV-outer
+          body with the counts before the slice, its own keys through the exact
+          window (token_outer_prefill.py:339-364);
+  repack  a cluster that outgrows its reservation lays the runs out again from
+          the current proportions (token_outer_prefill.py:366-392;
+          sbsa_gather_rows + sbsa_relayout_runs);
+  finish  the index and the packed store become the layer's decode state.
+
+Slices that start after the fit but within the dense prefix (start <= x*K)
+are still exact causal attention: their keys are read back in prompt order
+through the inverse map (sbsa_gather_rows), as the reference's fused body
+does (token_outer_prefill.py:155-159).
+
+Host reads: one per appended slice (the overflow flags, the reference's
+``bool((sizes + counts > reserve).any())``), and the cluster sizes at the
+fit and at a repack, from which the reserved layout is computed on the host.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib
+from .config import num_flat_clusters
+from .kv_outer import dense_causal_attention
+from .state import PACK_ALIGN, ProductPostingIndex
+
+
+def reserved_layout(sizes_ref: torch.Tensor, n_ref: int, total_tokens: int, width: int,
+                    align: int) -> torch.Tensor:
+    """Rows reserved per cluster, [Hkv, C] int64 on the host (token_outer_prefill.py:39-63).
+
+    Each cluster gets its share of ``total_tokens`` in the proportion it had
+    among the ``n_ref`` reference keys, rounded up to whole pages of
+    ``align`` rows and never below one page (an empty cluster may still
+    receive keys); the pages left in ``width`` are spread in the same
+    proportions.  Raises RuntimeError if the rounded shares alone exceed
+    ``width``.
+    """
+    align = max(int(align), 1)
+    share = sizes_ref.detach().to("cpu", torch.float64) * (float(total_tokens) / float(max(int(n_ref), 1)))
+    rows = torch.ceil(share / align).to(torch.int64).clamp_min(1) * align
+    for h in range(rows.shape[0]):
+        spare = int(width) - int(rows[h].sum())
+        if spare < 0:
+            raise RuntimeError(f"the reserved layout needs {int(rows[h].sum())} rows for KV head {h}; "
+                               f"the store holds {width}")
+        if spare >= align:
+            frac = share[h] / max(float(share[h].sum()), 1.0)
+            rows[h] += torch.floor(frac * (spare // align)).to(torch.int64) * align
+    return rows
+
+
+def nearest_cluster(keys: torch.Tensor, codebooks: torch.Tensor, *, router_pass: bool = True,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """[n, Hkv, D] keys -> [Hkv, n] int32 cluster ids (suffix_flush.py:154-170 after the
+    key router and routing_space): cosine in fp32, all-zero descriptors never chosen."""
+    n, hkv, d = keys.shape
+    c = int(codebooks.shape[2])
+    if keys.stride(-1) != 1:
+        keys = keys.contiguous()
+    if out is None:
+        out = torch.empty(hkv, n, dtype=torch.int32, device=keys.device)
+    _lib.call("sbsa_nearest_cluster", _lib.ptr(keys), n, keys.stride(0), keys.stride(1), hkv, d,
+              int(bool(router_pass)), _lib.ptr(codebooks), c, _lib.ptr(out), _lib.stream(keys.device))
+    return out
+
+
+def append_rows(ids: torch.Tensor, indptr: torch.Tensor, sizes: torch.Tensor,
+                reserve: torch.Tensor | None = None):
+    """Destination rows [Hkv, n] int32 of a slice's keys and per-cluster counts [Hkv, C]
+    (token_outer_prefill.py:66-87), plus the overflow flags [Hkv] when ``reserve`` is
+    given (bit 0: some cluster would outgrow its reservation)."""
+    hkv, n = ids.shape
+    c = int(sizes.shape[1])
+    dev = ids.device
+    rows = torch.empty(hkv, n, dtype=torch.int32, device=dev)
+    counts = torch.empty(hkv, c, dtype=torch.int32, device=dev)
+    flags = torch.zeros(hkv, dtype=torch.int32, device=dev)
+    res = None if reserve is None else reserve.to(device=dev, dtype=torch.int32).contiguous()
+    ids = ids.contiguous()
+    _lib.call("sbsa_append_rows", _lib.ptr(ids), n, hkv, c, _lib.ptr(indptr),
+              _lib.ptr(sizes), _lib.ptr(res), _lib.ptr(rows), _lib.ptr(counts), _lib.ptr(flags),
+              _lib.stream(dev))
+    return rows, counts, flags
+
+
+def gather_rows(index: ProductPostingIndex, first: int, n: int):
+    """K/V of positions first..first+n-1 in prompt order, [n, Hkv, D] each, read through
+    the inverse map."""
+    packed = index.packed_kv
+    hkv, d = packed.shape[2], packed.shape[3]
+    k = torch.empty(n, hkv, d, dtype=packed.dtype, device=packed.device)
+    v = torch.empty_like(k)
+    inv = index.inverse_positions()
+    _lib.call("sbsa_gather_rows", _lib.ptr(packed), packed.shape[1], hkv, d, _lib.ptr(inv),
+              inv.shape[1], int(first), int(n), _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1),
+              _lib.stream(packed.device))
+    return k, v
+
+
+class TokenOuterSnapshot:
+    """The counts the sparse body reads under this schedule (token_outer_prefill.py:90-125).
+
+    ``sizes`` [Hkv, C] are the keys appended by earlier slices, i.e. the rows
+    of every cluster visible to the slice being attended; the slice's own
+    keys are in the store but not counted here and are attended through its
+    exact window.
+    """
+
+    def __init__(self, index: ProductPostingIndex) -> None:
+        self.length = int(index.prompt_length)
+        self.sizes = torch.zeros_like(index.bucket_sizes)
+        self.chunk_start = 0
+
+    def advance(self, last_pos: int) -> torch.Tensor:
+        if int(last_pos) + 1 != self.chunk_start:
+            raise RuntimeError(
+                f"the token-outer snapshot holds the counts before position {self.chunk_start}; "
+                f"the body asked for position {last_pos}")
+        return self.sizes
+
+
+class TokenOuterPrefillSession:
+    """One sparse layer's share of a token-order prefill (token_outer_prefill.py:127-400).
+
+    ``slice`` takes the layer's projections of positions [start, stop) --
+    q_post [n, Hq, D], q_pre [n, Hq, D], k_pre, k_post, v [n, Hkv, D] -- where
+    the reference's ``slice(hidden_states, start, stop)`` projects them
+    itself; slices must come in order and cover the prompt.
+    """
+
+    def __init__(self, layer, tokens: int, chunk: int, *, fit_tokens: int | None = None) -> None:
+        cfg = layer.runtime_config
+        self.layer = layer
+        self.tokens = int(tokens)
+        self.chunk = int(chunk)
+        if self.chunk > int(cfg.query_chunk_size):
+            raise RuntimeError(
+                f"SEMBLO_PREFILL_CHUNK={self.chunk} must not exceed the query chunk "
+                f"({cfg.query_chunk_size}): a slice's keys are appended once, before its queries")
+        self.target = cfg.budget(self.tokens)
+        self.cap = int(cfg.dense_prefix_x) * self.target
+        if fit_tokens is None:
+            fit_tokens = int(os.environ.get("SEMBLO_TOKEN_OUTER_FIT_TOKENS", "65536"))
+        fit_tokens = min(int(fit_tokens), self.cap) if int(fit_tokens) > 0 else self.cap
+        self.fit_at = min(self.tokens, ((fit_tokens // self.chunk) + 1) * self.chunk)
+        self.stage_k = self.stage_v = self.stage_kpre = None
+        self.index: ProductPostingIndex | None = None
+        self.snapshot: TokenOuterSnapshot | None = None
+        self.reserve: torch.Tensor | None = None
+        self.repacks = 0
+        self.next_start = 0
+        layer.target_tokens = self.target
+
+    # -- per slice ------------------------------------------------------------------
+    def slice(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
+              out: torch.Tensor | None = None, timing=None) -> torch.Tensor:
+        if int(start) != self.next_start or not start < stop <= self.tokens:
+            raise RuntimeError(f"slice [{start}, {stop}) out of order (next start {self.next_start}, "
+                               f"{self.tokens} tokens)")
+        layer = self.layer
+        hq, hkv, d = layer.num_heads, layer.num_kv_heads, layer.head_dim
+        n = stop - start
+        q = q_post.reshape(n, hq, d)
+        qp = q_pre.reshape(n, hq, d)
+        kp = k_pre.reshape(n, hkv, d)
+        kk = k_post.reshape(n, hkv, d)
+        vv = v.reshape(n, hkv, d)
+        _lib.require_device(q, qp, kp, kk, vv)
+        if out is None:
+            out = torch.empty_like(q)
+        if self.index is None and start >= self.fit_at:
+            self._fit_and_pack()
+        if self.index is None:
+            self._stage(kp, kk, vv, start, stop)
+            self._count_dense(timing, start, n, hq, d)
+            dense_causal_attention(q, self.stage_k[:stop], self.stage_v[:stop], sm_scale=layer.scaling,
+                                   chunk_start=start, out=out, timing=timing)
+        else:
+            self._append(kp, kk, vv, start, stop)
+            self._attend(q, qp, kk, vv, start, stop, out, timing)
+        self.next_start = stop
+        return out
+
+    def finish(self) -> ProductPostingIndex:
+        if self.next_start != self.tokens:
+            raise RuntimeError(f"the prefill stopped at {self.next_start} of {self.tokens} tokens")
+        if self.index is None:
+            # the prompt ended before the fit point: fit on all of it
+            self.fit_at = self.tokens
+            self._fit_and_pack()
+        self.layer.adopt_index(self.index)
+        return self.index
+
+    # -- dense start ------------------------------------------------------------------
+    def _stage(self, kp, kk, vv, start, stop) -> None:
+        if self.stage_k is None:
+            shape = (self.fit_at,) + tuple(kk.shape[1:])
+            self.stage_k = kk.new_empty(shape)
+            self.stage_v = vv.new_empty(shape)
+            self.stage_kpre = kp.new_empty(shape)
+        self.stage_k[start:stop] = kk
+        self.stage_v[start:stop] = vv
+        self.stage_kpre[start:stop] = kp
+
+    @staticmethod
+    def _count_dense(timing, start, n, hq, d) -> None:
+        if timing is not None:
+            timing.add_flops(4.0 * d * hq * (n * (start + 1) + n * (n - 1) // 2))
+
+    # -- fit ----------------------------------------------------------------------------
+    def _fit_and_pack(self) -> None:
+        layer = self.layer
+        cfg = layer.runtime_config
+        p = self.fit_at
+        unit = int(os.environ.get("SEMBLO_FLAT_UNIT_TOKENS", cfg.flat_unit_tokens))
+        min_log2 = max(3, int(os.environ.get("SEMBLO_FLAT_MIN_CLUSTERS_LOG2", cfg.flat_min_clusters_log2)))
+        clusters = num_flat_clusters(self.tokens, unit, min_log2)   # the count the whole prompt gets
+        dev = self.stage_k.device
+        index = ProductPostingIndex.build(
+            self.stage_kpre[:p], torch.arange(p, device=dev), kmeans_sample_size=cfg.kmeans_sample_size,
+            codebook_seed=cfg.codebook_seed + cfg.layer_idx, flat_unit_tokens=unit,
+            flat_min_clusters_log2=min_log2, page_align=cfg.page_align, router_pass=True,
+            num_clusters=clusters)
+        hkv, d = self.stage_k.shape[1], self.stage_k.shape[2]
+        align = max(int(index.page_align), 1)
+        c = index.num_buckets
+        width = self.tokens + c * align
+        width += (-width) % PACK_ALIGN
+        self.reserve = reserved_layout(index.bucket_sizes, p, self.tokens, width, align)
+        indptr_h = torch.zeros(hkv, c + 1, dtype=torch.int32)
+        indptr_h[:, 1:] = torch.cumsum(self.reserve, 1).to(torch.int32)
+        indptr = indptr_h.to(dev)
+        packed = torch.zeros(2, width, hkv, d, dtype=self.stage_k.dtype, device=dev)
+        posting = torch.zeros(hkv, width, dtype=torch.int32, device=dev)
+        inverse = torch.zeros(hkv, self.tokens, dtype=torch.int32, device=dev)
+        old_rows = index.inverse_positions()                          # [Hkv, p] rows of the fitted layout
+        _lib.call("sbsa_relayout_runs", _lib.ptr(self.stage_k), _lib.ptr(self.stage_v),
+                  self.stage_k.stride(0), self.stage_k.stride(1), p, hkv, d, _lib.ptr(old_rows),
+                  old_rows.stride(0), _lib.ptr(index.bucket_indptr), _lib.ptr(indptr), c,
+                  _lib.ptr(packed), width, _lib.ptr(posting), width, _lib.ptr(inverse), self.tokens,
+                  _lib.stream(dev))
+        index.packed_kv = packed
+        index.posting_positions = posting
+        index.bucket_indptr = indptr
+        index._inverse_positions = inverse
+        index.prompt_length = self.tokens
+        index.max_position = self.tokens - 1
+        index.extras["reserve"] = self.reserve
+        self.index = index
+        self.snapshot = TokenOuterSnapshot(index)
+        self.stage_k = self.stage_v = self.stage_kpre = None
+
+    # -- append ---------------------------------------------------------------------------
+    def _append(self, kp, kk, vv, start, stop) -> None:
+        index = self.index
+        hkv, d = kk.shape[1], kk.shape[2]
+        c = index.num_buckets
+        n = stop - start
+        ids = nearest_cluster(kp, index.codebooks, router_pass=True)
+        rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
+        flags_h = flags.cpu()                                          # the one host read per slice
+        if bool((flags_h & 2).any()):
+            raise RuntimeError("a key was assigned outside the cluster range")
+        if bool((flags_h & 1).any()):
+            self._repack(start)
+            rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
+            if bool((flags.cpu() & 1).any()):
+                # The layout from the counts before the slice still leaves a cluster short
+                # (a burst of keys into a cluster that was small so far).  The reference
+                # appends anyway and its keys run into the next cluster's rows; here the
+                # runs are laid out again with the slice's own keys counted, which always fits.
+                self._repack(start, extra=counts, n_extra=n)
+                rows, counts, _ = append_rows(ids, index.bucket_indptr, index.bucket_sizes, None)
+        if kk.stride() != vv.stride() or kk.stride(-1) != 1:
+            kk, vv = kk.contiguous(), vv.contiguous()
+        packed, posting, inverse = index.packed_kv, index.posting_positions, index._inverse_positions
+        # the body sees the counts before this slice (snapshot.sizes); sizes advance past it
+        _lib.call("sbsa_append_kv", _lib.ptr(kk), _lib.ptr(vv), kk.stride(0), kk.stride(1), n, hkv, d,
+                  _lib.ptr(rows), int(start), _lib.ptr(packed), packed.shape[1], _lib.ptr(posting),
+                  posting.shape[1], _lib.ptr(inverse), inverse.shape[1], _lib.ptr(index.bucket_sizes),
+                  _lib.ptr(counts), c, _lib.ptr(self.snapshot.sizes), _lib.stream(kk.device))
+        self.snapshot.chunk_start = start
+
+    def _repack(self, n_so_far: int, extra: torch.Tensor | None = None, n_extra: int = 0) -> None:
+        """Lay the runs out again from the current proportions, in place
+        (token_outer_prefill.py:366-392).  The proportions are those of the
+        ``n_so_far`` keys in the store, plus ``extra`` [Hkv, C] keys about to be
+        appended (``n_extra`` of them) when given."""
+        index = self.index
+        packed = index.packed_kv
+        hkv, width, d = packed.shape[2], packed.shape[1], packed.shape[3]
+        c = index.num_buckets
+        align = max(int(index.page_align), 1)
+        ref_sizes = index.bucket_sizes if extra is None else index.bucket_sizes + extra
+        reserve = reserved_layout(ref_sizes, n_so_far + n_extra, self.tokens, width, align)
+        new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32)
+        new_ip[:, 1:] = torch.cumsum(reserve, 1).to(torch.int32)
+        new_ip = new_ip.to(packed.device)
+        k_tmp, v_tmp = gather_rows(index, 0, n_so_far)
+        old_rows = index._inverse_positions[:, :n_so_far].clone()
+        _lib.call("sbsa_relayout_runs", _lib.ptr(k_tmp), _lib.ptr(v_tmp), k_tmp.stride(0), k_tmp.stride(1),
+                  n_so_far, hkv, d, _lib.ptr(old_rows), old_rows.stride(0), _lib.ptr(index.bucket_indptr),
+                  _lib.ptr(new_ip), c, _lib.ptr(packed), width, _lib.ptr(index.posting_positions),
+                  index.posting_positions.shape[1], _lib.ptr(index._inverse_positions),
+                  index._inverse_positions.shape[1], _lib.stream(packed.device))
+        index.bucket_indptr.copy_(new_ip)                             # same address as before
+        self.reserve = reserve
+        index.extras["reserve"] = reserve
+        self.repacks += 1
+        print(f"[semblo_amd] token-order prefill layer {self.layer.layer_idx}: a cluster outgrew its "
+              f"reservation at position {n_so_far:,}; the store was laid out again "
+              f"(repack {self.repacks})", flush=True)
+
+    # -- attention of an appended slice ---------------------------------------------------
+    def _attend(self, q, qp, kk, vv, start, stop, out, timing) -> None:
+        from .fused_prefill import fused_chunk_attention
+        layer = self.layer
+        cfg = layer.runtime_config
+        n = stop - start
+        if start <= self.cap:
+            # within the dense prefix: exact causal attention over the store read in prompt order
+            k_all, v_all = gather_rows(self.index, 0, stop)
+            self._count_dense(timing, start, n, q.shape[1], q.shape[2])
+            dense_causal_attention(q, k_all, v_all, sm_scale=layer.scaling, chunk_start=start, out=out,
+                                   timing=timing)
+            return
+        qs = layer._query_state(qp)
+        fused_chunk_attention(q, qs, self.index, None, self.snapshot, start, stop - 1,
+                              temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
+                              target_tokens=self.target, sm_scale=layer.scaling, iters=cfg.iters,
+                              dense_prefix_x=cfg.dense_prefix_x, out=out, timing=timing,
+                              window_kv=(kk, vv))

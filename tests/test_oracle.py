@@ -127,3 +127,91 @@ def test_reverse_index_is_the_transpose():
             got = qvals[e0:e0 + n].tolist()
             want = torch.nonzero(sel[:, h, c] & live[h, c]).flatten().tolist()
             assert got == want
+
+
+# ---- S10: token-order append ---------------------------------------------------
+
+def test_reserved_layout_is_proportional_paged_and_fits():
+    """The properties the reference's own test asserts (test_token_outer_prefill.py:14-27)
+    and one case worked by hand."""
+    sizes = torch.tensor([[100, 0, 300, 20], [50, 150, 0, 200]])
+    width = 16 * 200
+    reserve = ref.reserved_layout(sizes, n_ref=420, total_tokens=2000, width=width, align=16)
+    assert reserve.shape == sizes.shape
+    assert bool((reserve % 16 == 0).all()) and bool((reserve >= 16).all())
+    assert bool((reserve.sum(dim=1) <= width).all())
+    assert bool((reserve.double() >= sizes.double() * (2000 / 420)).all())
+    assert 2.5 < reserve[0, 2].item() / reserve[0, 0].item() < 3.5
+    # head 0 by hand: shares 476.19, 0, 1428.57, 95.24 -> pages 30, 1, 90, 6 (2032 rows);
+    # the 73 spare pages split 0.238 / 0 / 0.714 / 0.048 -> 17, 0, 52, 3 more pages
+    assert reserve[0].tolist() == [752, 16, 2272, 144]
+
+
+def test_reserved_layout_refuses_a_store_too_small():
+    with pytest.raises(RuntimeError):
+        ref.reserved_layout(torch.tensor([[10, 10]]), n_ref=20, total_tokens=1000, width=512,
+                            align=16)
+
+
+def test_append_rows_known_answers():
+    """test_token_outer_prefill.py:30-38 of the reference."""
+    indptr = torch.tensor([[0, 32, 64, 96]], dtype=torch.int32)
+    sizes = torch.tensor([[5, 0, 30]], dtype=torch.int32)
+    rows, counts = ref.append_rows(torch.tensor([[2, 0, 2, 1, 0]]), indptr, sizes)
+    assert counts.tolist() == [[2, 1, 2]]
+    assert rows.tolist() == [[94, 5, 95, 32, 6]]
+
+
+def test_append_rows_matches_a_stable_sort():
+    """The scan against the rank of each key in a stable sort of the ids."""
+    gen = torch.Generator().manual_seed(5)
+    c, n = 64, 3000
+    ids = torch.randint(0, c, (2, n), generator=gen)
+    sizes = torch.randint(0, 50, (2, c), generator=gen)
+    indptr = torch.zeros(2, c + 1, dtype=torch.int64)
+    indptr[:, 1:] = torch.cumsum(sizes + 200, 1)
+    rows, counts = ref.append_rows(ids, indptr, sizes)
+    for h in range(2):
+        order = torch.argsort(ids[h], stable=True)
+        cnt = torch.bincount(ids[h], minlength=c)
+        first = torch.cumsum(cnt, 0) - cnt
+        rank = torch.empty(n, dtype=torch.int64)
+        rank[order] = torch.arange(n) - first[ids[h][order]]
+        assert torch.equal(rows[h], indptr[h, ids[h]] + sizes[h, ids[h]] + rank)
+        assert torch.equal(counts[h], cnt)
+
+
+def test_nearest_cluster_is_the_fp64_argmax_and_skips_dead_descriptors():
+    gen = torch.Generator().manual_seed(6)
+    n, c, d = 400, 128, 64
+    keys = torch.randn(n, d, generator=gen).to(torch.bfloat16)
+    cents = torch.nn.functional.normalize(torch.randn(c, d, generator=gen), dim=-1)
+    cents[7] = 0
+    cents[90] = 0
+    cb = torch.stack(list(cents.chunk(2, dim=-1))).to(torch.bfloat16)      # [2, C, d/2]
+    ids, sim = ref.nearest_cluster(keys, cb, return_sim=True)
+    # fp64 restatement of the same chain
+    unit = keys.double() / keys.double().norm(dim=-1, keepdim=True)
+    unit = unit.to(torch.bfloat16).double()
+    unit = unit / unit.norm(dim=-1, keepdim=True)
+    c64 = torch.cat([cb[0], cb[1]], dim=-1).double()
+    s64 = unit @ c64.t()
+    s64[:, [7, 90]] = -math.inf
+    top2 = s64.topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 1e-5
+    assert int(clear.sum()) > n * 0.9
+    assert torch.equal(ids[clear], s64.argmax(-1)[clear])
+    assert not bool(((ids == 7) | (ids == 90)).any())
+    # equal maxima: the first index
+    dup = torch.cat([cb, cb], dim=1)                                          # clusters c..2c-1 repeat
+    assert bool((ref.nearest_cluster(keys, dup) < c).all())
+
+
+def test_relayout_keeps_each_key_at_its_offset_in_the_new_run():
+    sizes = torch.tensor([[3, 0, 5]])
+    old_ip = torch.tensor([[0, 16, 16, 32]])
+    new_ip = torch.tensor([[0, 48, 64, 112]])
+    old_rows = torch.tensor([[0, 16, 1, 17, 18, 2, 19, 20]])   # positions 0..7
+    new = ref.relayout_rows(old_rows, old_ip, new_ip)
+    assert new.tolist() == [[0, 64, 1, 65, 66, 2, 67, 68]]
+    assert int(sizes.sum()) == new.shape[1]
