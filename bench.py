@@ -65,12 +65,16 @@ def _log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def run_prefill(layer, inp, timing=None):
-    from semblo_amd import kv_outer  # noqa: F401
+def run_prefill(layer, inp, conf, timing=None, store_timing=None):
     length = inp.q.shape[0]
     out = torch.empty(length, layer.num_heads * layer.head_dim, dtype=inp.q.dtype,
                       device=inp.q.device)
-    layer.prefill(inp.q, inp.q, inp.k, inp.k, inp.v, out, timing=timing)
+    if conf.get("order") == "token":
+        layer.prefill_token_order(inp.q, inp.q, inp.k, inp.k, inp.v, out, conf["chunk"],
+                                  timing=timing, store_timing=store_timing,
+                                  fit_tokens=conf["fit_tokens"])
+    else:
+        layer.prefill(inp.q, inp.q, inp.k, inp.k, inp.v, out, timing=timing)
     return out
 
 
@@ -218,22 +222,20 @@ def main():
     result = {}
     if args.only in ("all", "prefill"):
         for i in range(args.warmup):
-            run_prefill(layer, inp)
+            run_prefill(layer, inp, conf)
             torch.cuda.synchronize()
             _log(f"warm-up {i} done")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run_prefill(layer, inp)
+            run_prefill(layer, inp, conf)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / max(args.steps, 1)
         _log(f"prefill {ms:.2f} ms/layer")
         # one instrumented pass: attention kernel time and FLOPs, and the build time
         timing = KernelTiming()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        ev[0].record()
-        run_prefill(layer, inp, timing=timing)
-        ev[1].record()
+        store = KernelTiming() if conf.get("order") == "token" else None
+        run_prefill(layer, inp, conf, timing=timing, store_timing=store)
         torch.cuda.synchronize()
         attn_ms = timing.total_ms()
         flops = timing.total_flops()
@@ -242,9 +244,18 @@ def main():
                       launches=timing.launches())
         _log(f"attention kernel {attn_ms:.2f} ms over {timing.launches()} launches, "
              f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s")
+        if store is not None:
+            st_ms = store.total_ms()
+            st_bytes = store.total_flops()           # the store timing collects bytes
+            sess = layer.last_session
+            result.update(store_ms=st_ms, store_bytes=st_bytes, store_slices=store.launches() // 2,
+                          repacks=sess.repacks, fit_at=sess.fit_at)
+            _log(f"store kernels {st_ms:.2f} ms over {store.launches() // 2} appended slices, "
+                 f"{st_bytes / 1e9:.2f} GB -> {st_bytes / (st_ms * 1e-3) / 1e9:.0f} GB/s; "
+                 f"{sess.repacks} repacks")
     if args.only in ("all", "decode"):
         if layer.arena is None:
-            run_prefill(layer, inp)
+            run_prefill(layer, inp, conf)
         graph, outs = decode_graph(layer, inp, dsteps, cfg)
         graph.replay()
         torch.cuda.synchronize()
@@ -271,6 +282,17 @@ def main():
     if not args.no_cpu_baseline and args.only in ("all", "prefill"):
         cpu = cpu_baseline(inp, layer, cfg, args.cpu_sample_queries)
         _log(f"cpu baseline {cpu['value']} ms/layer on {cpu['cores']} threads")
+    if conf.get("order") == "token":
+        workload = (f"config {args.config}: one full-attention layer, L={length}, Hq={hq}, Hkv={hkv}, "
+                    f"D={d}, K={layer.target_tokens}, token-order streamed prefill in {conf['chunk']}-"
+                    f"token slices, clusters fitted on the first {conf['fit_tokens']} (+1 slice) "
+                    f"positions, later keys appended to the fixed clusters; {dsteps} "
+                    f"hipGraph-captured decode steps")
+    else:
+        workload = (f"config {args.config}: one full-attention layer, L={length}, Hq={hq}, "
+                    f"Hkv={hkv}, D={d}, K={layer.target_tokens}, chunk {conf['chunk']}, block build + "
+                    f"{length // conf['chunk']}-chunk sparse prefill; {dsteps} hipGraph-captured "
+                    f"decode steps")
     line = {
         "metric": "sparse prefill ms/layer @128K + decode us/step/layer; % MFMA / HBM roofline",
         "value": round(result.get("prefill_ms", float("nan")), 3),
@@ -284,11 +306,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (Gaussian-mixture keys/queries, N(0,1) values, seeded)",
-        "config": {"workload": f"config {args.config}: one full-attention layer, L={length}, "
-                               f"Hq={hq}, Hkv={hkv}, D={d}, K={layer.target_tokens}, "
-                               f"chunk {conf['chunk']}, block build + 16-chunk sparse prefill; "
-                               f"{dsteps} hipGraph-captured decode steps",
-                   "prompt_tokens": length, "decode_steps": dsteps},
+        "config": {"workload": workload, "prompt_tokens": length, "decode_steps": dsteps},
         "decode_us_per_step": round(result["decode_us"], 3) if "decode_us" in result else None,
         "roofline": None if "achieved" not in result else {
             "bound": "mfma", "achieved": round(result["achieved"], 1), "peak": PEAK_BF16_TFLOPS,
@@ -304,6 +322,16 @@ def main():
             "scope": "whole step (select + attend + merge) from graph replay time"},
         "cpu_baseline": cpu,
     }
+    if "store_ms" in result:
+        gbs = result["store_bytes"] / (result["store_ms"] * 1e-3) / 1e9
+        line["store_roofline"] = {
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+            "kernels": "nearest_cluster_kernel + append_rows_kernel + copy_rows_kernel + "
+                       "append_index_kernel",
+            "kernel_ms_per_layer": round(result["store_ms"], 3),
+            "appended_slices": result["store_slices"], "bytes_per_layer": result["store_bytes"],
+            "repacks": result["repacks"], "fit_at": result["fit_at"]}
     print(json.dumps(line), flush=True)
 
 

@@ -273,6 +273,19 @@ int sbsa_gather_rows(const void* packed, int64_t packed_len, int num_kv_heads, i
                      const int32_t* inverse, int64_t inverse_ld, int64_t first, int64_t n, void* key_out,
                      void* value_out, int64_t stride_tok, int64_t stride_head, hipStream_t stream);
 
+/* The row moves of _repack (semblo/vllm_plugin/token_outer_prefill.py:366-392)
+ * into the other buffer of a double-buffered store, in one pass:
+ * dst_packed[t, new row, h] = src_packed[t, old_rows[h, i], h] for positions
+ * i < n, with the new row found as in sbsa_relayout_runs (written to inverse,
+ * which must not overlap old_rows) and posting[h, new row] = i.  Both stores
+ * are [2, packed_len, Hkv, dim]; rows of dst that no key lands on keep what
+ * they held. */
+int sbsa_repack_runs(const void* src_packed, void* dst_packed, int64_t packed_len, int num_kv_heads,
+                     int dim, int64_t n, const int32_t* old_rows, int64_t old_rows_ld,
+                     const int32_t* old_indptr, const int32_t* new_indptr, int num_clusters,
+                     int32_t* posting, int64_t posting_width, int32_t* inverse, int64_t inverse_ld,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

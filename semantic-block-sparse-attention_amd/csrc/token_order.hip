@@ -12,7 +12,8 @@
 //   token_outer_prefill.py:66-87         append_rows (stable rank in position order)
 //   token_outer_prefill.py:339-364       _append (K/V, posting and inverse rows, sizes)
 //   token_outer_prefill.py:284-318       _fit_and_pack (fitted keys into the reserved runs)
-//   token_outer_prefill.py:366-392       _repack (the runs laid out again, in place)
+//   token_outer_prefill.py:366-392       _repack (the runs laid out again; here into the
+//                                        other buffer of a double-buffered store)
 #include "sbsa_common.h"
 
 namespace {
@@ -355,6 +356,31 @@ __global__ void gather_rows_kernel(const bf16_t* __restrict__ packed, int64_t pa
   }
 }
 
+// dst[t, new_rows[h, i], h, :] = src[t, old_rows[h, i], h, :] (a repack into the
+// other buffer of a double-buffered store; rows out of range are skipped).
+__global__ void move_rows_kernel(const bf16_t* __restrict__ src, bf16_t* __restrict__ dst,
+                                 int64_t packed_len, int hkv, int dim, int64_t n,
+                                 const int32_t* __restrict__ old_rows, int64_t old_ld,
+                                 const int32_t* __restrict__ new_rows, int64_t new_ld) {
+  const int chunks = dim / 8;
+  const int64_t per_plane = n * hkv * chunks;
+  const int64_t total = 2 * per_plane;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = e / per_plane;
+    const int64_t rem = e - t * per_plane;
+    const int64_t i = rem / (hkv * chunks);
+    const int hc = (int)(rem - i * (hkv * chunks));
+    const int h = hc / chunks, ch = hc - h * chunks;
+    const int64_t ro = old_rows[(int64_t)h * old_ld + i];
+    const int64_t rn = new_rows[(int64_t)h * new_ld + i];
+    if (ro < 0 || ro >= packed_len || rn < 0 || rn >= packed_len) continue;
+    const int64_t plane = t * packed_len;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(src + ((plane + ro) * hkv + h) * dim + ch * 8);
+    *reinterpret_cast<u32x4_t*>(dst + ((plane + rn) * hkv + h) * dim + ch * 8) = v;
+  }
+}
+
 unsigned grid_for(int64_t work, int per_block) {
   int64_t b = (work + per_block - 1) / per_block;
   if (b > 8192) b = 8192;
@@ -480,6 +506,33 @@ int sbsa_gather_rows(const void* packed, int64_t packed_len, int num_kv_heads, i
   hipLaunchKernelGGL(gather_rows_kernel, dim3(grid_for(moves, 256)), dim3(256), 0, stream,
                      (const bf16_t*)packed, packed_len, num_kv_heads, dim, inverse, inverse_ld, first, n,
                      (bf16_t*)key_out, (bf16_t*)value_out, stride_tok, stride_head);
+  SBSA_CHECK_LAUNCH();
+  return SBSA_OK;
+}
+
+int sbsa_repack_runs(const void* src_packed, void* dst_packed, int64_t packed_len, int num_kv_heads,
+                     int dim, int64_t n, const int32_t* old_rows, int64_t old_rows_ld,
+                     const int32_t* old_indptr, const int32_t* new_indptr, int num_clusters,
+                     int32_t* posting, int64_t posting_width, int32_t* inverse, int64_t inverse_ld,
+                     hipStream_t stream) {
+  if (!src_packed || !dst_packed || !old_rows || !old_indptr || !new_indptr || !posting || !inverse)
+    return SBSA_ERR_ARG;
+  if (n < 0 || num_kv_heads < 1 || num_clusters < 1 || dim % 8 || dim < 8) return SBSA_ERR_ARG;
+  if (!aligned16(src_packed) || !aligned16(dst_packed) || src_packed == dst_packed) return SBSA_ERR_ARG;
+  if (old_rows_ld < n || inverse_ld < n) return SBSA_ERR_CAPACITY;
+  const char* a0 = (const char*)old_rows;
+  const char* a1 = a0 + (size_t)num_kv_heads * old_rows_ld * 4;
+  const char* b0 = (const char*)inverse;
+  const char* b1 = b0 + (size_t)num_kv_heads * inverse_ld * 4;
+  if (a0 < b1 && b0 < a1) return SBSA_ERR_ARG;
+  if (n == 0) return SBSA_OK;
+  hipLaunchKernelGGL(relayout_map_kernel, dim3(grid_for(n * num_kv_heads, 256)), dim3(256), 0, stream,
+                     old_rows, old_rows_ld, n, num_kv_heads, old_indptr, new_indptr, num_clusters, inverse,
+                     inverse_ld, posting, posting_width);
+  const int64_t moves = 2 * n * num_kv_heads * (dim / 8);
+  hipLaunchKernelGGL(move_rows_kernel, dim3(grid_for(moves, 256)), dim3(256), 0, stream,
+                     (const bf16_t*)src_packed, (bf16_t*)dst_packed, packed_len, num_kv_heads, dim, n,
+                     old_rows, old_rows_ld, inverse, inverse_ld);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }

@@ -53,6 +53,7 @@ SIGNATURES = {
     "sbsa_relayout_runs": (I32, [P, P, I64, I64, I64, I32, I32, P, I64, P, P, I32, P, I64, P, I64,
                                  P, I64, P]),
     "sbsa_gather_rows": (I32, [P, I64, I32, I32, P, I64, I64, I64, P, P, I64, I64, P]),
+    "sbsa_repack_runs": (I32, [P, P, I64, I32, I32, I64, P, I64, P, P, I32, P, I64, P, I64, P]),
 }
 
 ERRORS = {1: "bad argument", 2: "unsupported shape", 3: "kernel launch failed",

@@ -95,7 +95,7 @@ class SembloAttention:
                                  suffix_splits=cfg.decode_suffix_splits)
 
     def prefill_token_order(self, q_post, q_pre, k_pre, k_post, v, output, chunk: int,
-                            timing=None, **kw) -> torch.Tensor:
+                            timing=None, store_timing=None, **kw) -> torch.Tensor:
         """The whole prompt in token order, one ``chunk``-position slice after another
         (streamed_prefill.py:547-593 for one layer)."""
         length = q_post.shape[0]
@@ -107,7 +107,8 @@ class SembloAttention:
             session.slice(q_post.view(length, hq, d)[start:stop], q_pre.view(length, hq, d)[start:stop],
                           k_pre.view(length, hkv, d)[start:stop], k_post.view(length, hkv, d)[start:stop],
                           v.view(length, hkv, d)[start:stop], start, stop, out=out[start:stop],
-                          timing=timing)
+                          timing=timing, store_timing=store_timing)
+        self.last_session = session
         session.finish()
         return output
 

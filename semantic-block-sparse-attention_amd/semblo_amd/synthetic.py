@@ -89,5 +89,6 @@ CONFIGS = {
     3: dict(length=131072, hq=16, hkv=4, d=256, mixtures=1024, seg=(16, 2048), log_uniform=True,
             sinks=4, dtype=torch.bfloat16, chunk=8192, decode_steps=256),
     4: dict(length=524288, hq=16, hkv=4, d=256, mixtures=1024, seg=(16, 2048), log_uniform=True,
-            sinks=0, dtype=torch.bfloat16, chunk=8192, decode_steps=128),
+            sinks=0, dtype=torch.bfloat16, chunk=8192, decode_steps=128,
+            order="token", fit_tokens=65536),
 }

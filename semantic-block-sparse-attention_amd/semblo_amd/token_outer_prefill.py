@@ -18,7 +18,7 @@ every array operation on the GPU through libsbsa.  In each sparse layer:
           window (token_outer_prefill.py:339-364);
   repack  a cluster that outgrows its reservation lays the runs out again from
           the current proportions (token_outer_prefill.py:366-392;
-          sbsa_gather_rows + sbsa_relayout_runs);
+          sbsa_repack_runs into the other buffer of a double-buffered store);
   finish  the index and the packed store become the layer's decode state.
 
 Slices that start after the fit but within the dense prefix (start <= x*K)
@@ -166,12 +166,18 @@ class TokenOuterPrefillSession:
         self.snapshot: TokenOuterSnapshot | None = None
         self.reserve: torch.Tensor | None = None
         self.repacks = 0
+        self.repacks_with_slice = 0                 # repacks whose layout counts the slice's keys
         self.next_start = 0
+        self._spare: torch.Tensor | None = None     # the other buffer of the store, after a repack
+        self.verbose = os.environ.get("SEMBLO_VERBOSE", "0") == "1"
         layer.target_tokens = self.target
 
     # -- per slice ------------------------------------------------------------------
     def slice(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
-              out: torch.Tensor | None = None, timing=None) -> torch.Tensor:
+              out: torch.Tensor | None = None, timing=None, store_timing=None) -> torch.Tensor:
+        """Attention of positions [start, stop) into ``out`` [n, Hq, D].  ``timing``
+        brackets the attention launches, ``store_timing`` the store kernels of an
+        append (assignment, rows, K/V writes), each with HIP events."""
         if int(start) != self.next_start or not start < stop <= self.tokens:
             raise RuntimeError(f"slice [{start}, {stop}) out of order (next start {self.next_start}, "
                                f"{self.tokens} tokens)")
@@ -194,7 +200,7 @@ class TokenOuterPrefillSession:
             dense_causal_attention(q, self.stage_k[:stop], self.stage_v[:stop], sm_scale=layer.scaling,
                                    chunk_start=start, out=out, timing=timing)
         else:
-            self._append(kp, kk, vv, start, stop)
+            self._append(kp, kk, vv, start, stop, store_timing)
             self._attend(q, qp, kk, vv, start, stop, out, timing)
         self.next_start = stop
         return out
@@ -206,6 +212,7 @@ class TokenOuterPrefillSession:
             # the prompt ended before the fit point: fit on all of it
             self.fit_at = self.tokens
             self._fit_and_pack()
+        self._spare = None
         self.layer.adopt_index(self.index)
         return self.index
 
@@ -269,65 +276,88 @@ class TokenOuterPrefillSession:
         self.stage_k = self.stage_v = self.stage_kpre = None
 
     # -- append ---------------------------------------------------------------------------
-    def _append(self, kp, kk, vv, start, stop) -> None:
+    def _append(self, kp, kk, vv, start, stop, store_timing=None) -> None:
         index = self.index
         hkv, d = kk.shape[1], kk.shape[2]
         c = index.num_buckets
         n = stop - start
+        s = _lib.stream(kk.device)
+        if store_timing is not None:
+            store_timing.begin(s)
         ids = nearest_cluster(kp, index.codebooks, router_pass=True)
         rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
-        flags_h = flags.cpu()                                          # the one host read per slice
+        if store_timing is not None:
+            store_timing.end(s)
+        # the one host read per slice: flags, the slice's counts and the sizes so far
+        host = torch.cat([flags, counts.flatten(), index.bucket_sizes.flatten()]).cpu()
+        flags_h = host[:hkv]
         if bool((flags_h & 2).any()):
             raise RuntimeError("a key was assigned outside the cluster range")
         if bool((flags_h & 1).any()):
-            self._repack(start)
-            rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
-            if bool((flags.cpu() & 1).any()):
-                # The layout from the counts before the slice still leaves a cluster short
-                # (a burst of keys into a cluster that was small so far).  The reference
-                # appends anyway and its keys run into the next cluster's rows; here the
-                # runs are laid out again with the slice's own keys counted, which always fits.
-                self._repack(start, extra=counts, n_extra=n)
-                rows, counts, _ = append_rows(ids, index.bucket_indptr, index.bucket_sizes, None)
+            counts_h = host[hkv:hkv + hkv * c].view(hkv, c).to(torch.int64)
+            sizes_h = host[hkv + hkv * c:].view(hkv, c).to(torch.int64)
+            width = index.packed_kv.shape[1]
+            align = max(int(index.page_align), 1)
+            reserve = reserved_layout(sizes_h, start, self.tokens, width, align)
+            if bool((sizes_h + counts_h > reserve).any()):
+                # The reference's layout, from the counts before the slice, still leaves a
+                # cluster short (a burst of keys into a cluster that was small so far): the
+                # reference appends anyway and those keys run into the next cluster's rows.
+                # Here the runs are laid out with the slice's own keys counted, which
+                # always fits; the reference's intermediate layout is skipped.
+                reserve = reserved_layout(sizes_h + counts_h, start + n, self.tokens, width, align)
+                self.repacks_with_slice += 1
+            self._repack(start, reserve)
+            rows, counts, _ = append_rows(ids, index.bucket_indptr, index.bucket_sizes, None)
         if kk.stride() != vv.stride() or kk.stride(-1) != 1:
             kk, vv = kk.contiguous(), vv.contiguous()
         packed, posting, inverse = index.packed_kv, index.posting_positions, index._inverse_positions
+        if store_timing is not None:
+            store_timing.begin(s)
         # the body sees the counts before this slice (snapshot.sizes); sizes advance past it
         _lib.call("sbsa_append_kv", _lib.ptr(kk), _lib.ptr(vv), kk.stride(0), kk.stride(1), n, hkv, d,
                   _lib.ptr(rows), int(start), _lib.ptr(packed), packed.shape[1], _lib.ptr(posting),
                   posting.shape[1], _lib.ptr(inverse), inverse.shape[1], _lib.ptr(index.bucket_sizes),
-                  _lib.ptr(counts), c, _lib.ptr(self.snapshot.sizes), _lib.stream(kk.device))
+                  _lib.ptr(counts), c, _lib.ptr(self.snapshot.sizes), s)
+        if store_timing is not None:
+            store_timing.end(s)
+            # algorithmic bytes: the slice's pre-RoPE keys and the descriptors read by the
+            # assignment; K and V read and written once; ids, rows, posting and inverse entries
+            store_timing.add_flops(float(n * hkv * d * 2 + hkv * c * d * 2 + 4 * n * hkv * d * 2
+                                         + 4 * 5 * n * hkv))
         self.snapshot.chunk_start = start
 
-    def _repack(self, n_so_far: int, extra: torch.Tensor | None = None, n_extra: int = 0) -> None:
-        """Lay the runs out again from the current proportions, in place
-        (token_outer_prefill.py:366-392).  The proportions are those of the
-        ``n_so_far`` keys in the store, plus ``extra`` [Hkv, C] keys about to be
-        appended (``n_extra`` of them) when given."""
+    def _repack(self, n_so_far: int, reserve: torch.Tensor) -> None:
+        """Lay the runs out again as ``reserve`` [Hkv, C] says (token_outer_prefill.py:366-392).
+
+        The store is double-buffered: the keys of positions < ``n_so_far`` move in
+        one pass from their rows in the current buffer to their rows in the other
+        (sbsa_repack_runs), which then becomes the store."""
         index = self.index
         packed = index.packed_kv
         hkv, width, d = packed.shape[2], packed.shape[1], packed.shape[3]
         c = index.num_buckets
-        align = max(int(index.page_align), 1)
-        ref_sizes = index.bucket_sizes if extra is None else index.bucket_sizes + extra
-        reserve = reserved_layout(ref_sizes, n_so_far + n_extra, self.tokens, width, align)
         new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32)
         new_ip[:, 1:] = torch.cumsum(reserve, 1).to(torch.int32)
         new_ip = new_ip.to(packed.device)
-        k_tmp, v_tmp = gather_rows(index, 0, n_so_far)
+        if self._spare is None:
+            self._spare = torch.zeros_like(packed)
+        dst = self._spare
         old_rows = index._inverse_positions[:, :n_so_far].clone()
-        _lib.call("sbsa_relayout_runs", _lib.ptr(k_tmp), _lib.ptr(v_tmp), k_tmp.stride(0), k_tmp.stride(1),
-                  n_so_far, hkv, d, _lib.ptr(old_rows), old_rows.stride(0), _lib.ptr(index.bucket_indptr),
-                  _lib.ptr(new_ip), c, _lib.ptr(packed), width, _lib.ptr(index.posting_positions),
-                  index.posting_positions.shape[1], _lib.ptr(index._inverse_positions),
-                  index._inverse_positions.shape[1], _lib.stream(packed.device))
+        _lib.call("sbsa_repack_runs", _lib.ptr(packed), _lib.ptr(dst), width, hkv, d, n_so_far,
+                  _lib.ptr(old_rows), old_rows.stride(0), _lib.ptr(index.bucket_indptr), _lib.ptr(new_ip),
+                  c, _lib.ptr(index.posting_positions), index.posting_positions.shape[1],
+                  _lib.ptr(index._inverse_positions), index._inverse_positions.shape[1],
+                  _lib.stream(packed.device))
+        index.packed_kv, self._spare = dst, packed
         index.bucket_indptr.copy_(new_ip)                             # same address as before
         self.reserve = reserve
         index.extras["reserve"] = reserve
         self.repacks += 1
-        print(f"[semblo_amd] token-order prefill layer {self.layer.layer_idx}: a cluster outgrew its "
-              f"reservation at position {n_so_far:,}; the store was laid out again "
-              f"(repack {self.repacks})", flush=True)
+        if self.verbose:
+            print(f"[semblo_amd] token-order prefill layer {self.layer.layer_idx}: a cluster outgrew "
+                  f"its reservation at position {n_so_far:,}; the store was laid out again "
+                  f"(repack {self.repacks})", flush=True)
 
     # -- attention of an appended slice ---------------------------------------------------
     def _attend(self, q, qp, kk, vv, start, stop, out, timing) -> None:

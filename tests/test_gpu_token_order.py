@@ -118,30 +118,31 @@ def _oracle_store(inp, tokens, chunk, fit_at, c, seed, ids_by_slice, align=16):
     inverse[:, :fit_at] = rows
     inverse_fit = inverse.clone()
     sizes = built["sizes"].to(torch.int64).clone()
-    before, repacks, trail = [], 0, []
+    before, repacks, trail, with_slice = [], 0, [], 0
     for start in range(fit_at, tokens, chunk):
         stop = min(tokens, start + chunk)
         ids = ids_by_slice[start].long()
         r, counts = ref.append_rows(ids, indptr, sizes)
         if bool((sizes + counts > reserve).any()):
-            # the reference's repack, from the counts before the slice; if the slice
-            # still does not fit, once more with its keys counted
-            for ref_sizes, n_ref in ((sizes, start), (sizes + counts, stop)):
-                reserve = ref.reserved_layout(ref_sizes, n_ref, tokens, width, align)
-                new_ip = torch.zeros_like(indptr)
-                new_ip[:, 1:] = torch.cumsum(reserve, 1)
-                inverse[:, :start] = ref.relayout_rows(inverse[:, :start], indptr, new_ip)
-                indptr = new_ip
-                repacks += 1
-                r, counts = ref.append_rows(ids, indptr, sizes)
-                if not bool((sizes + counts > reserve).any()):
-                    break
+            # the reference's layout from the counts before the slice; if the slice would
+            # still not fit, the layout with its keys counted instead
+            reserve = ref.reserved_layout(sizes, start, tokens, width, align)
+            if bool((sizes + counts > reserve).any()):
+                reserve = ref.reserved_layout(sizes + counts, stop, tokens, width, align)
+                with_slice += 1
+            new_ip = torch.zeros_like(indptr)
+            new_ip[:, 1:] = torch.cumsum(reserve, 1)
+            inverse[:, :start] = ref.relayout_rows(inverse[:, :start], indptr, new_ip)
+            indptr = new_ip
+            repacks += 1
+            r, counts = ref.append_rows(ids, indptr, sizes)
+            assert not bool((sizes + counts > reserve).any())
         inverse[:, start:stop] = r
         trail.append(inverse.clone())
         before.append(sizes.clone())
         sizes = sizes + counts
     return dict(codebooks=built["codebooks"], indptr=indptr, sizes=sizes, inverse=inverse,
-                before=before, repacks=repacks, width=width, trail=trail,
+                before=before, repacks=repacks, with_slice=with_slice, width=width, trail=trail,
                 fitted=inverse_fit)
 
 
@@ -216,6 +217,7 @@ def test_token_order_session_store_and_attention(cfg):
     _first_divergence(_run_session.trail, exp, fit_at, cfg["chunk"])
     assert torch.equal(inv, exp["inverse"])
     assert session.repacks == exp["repacks"]
+    assert session.repacks_with_slice == exp["with_slice"]
     for i, start in enumerate(sorted(before)):
         assert torch.equal(before[start].long(), exp["before"][i])
     posting = index.posting_positions.cpu().long()
@@ -257,7 +259,7 @@ def test_token_order_session_store_and_attention(cfg):
         # near-tie selection differences move a handful of rows
         assert int(bad_q.sum()) <= 2, f"slice {start}: {int(bad_q.sum())} queries off"
     print(f"{cfg}: fit at {fit_at}, {len(ids_by_slice)} appended slices, {moved} near-tie ids, "
-          f"{session.repacks} repacks, {bad_total} queries beyond tolerance (near-tie selections)")
+          f"{session.repacks} repacks ({session.repacks_with_slice} counting the slice), {bad_total} queries beyond tolerance (near-tie selections)")
     assert layer.arena is not None and layer.arena.prompt_length == tokens
 
 
@@ -276,6 +278,7 @@ def test_token_order_repacks_when_a_cluster_outgrows_its_reservation():
     c = index.num_buckets
     exp = _oracle_store(inp, cfg["tokens"], cfg["chunk"], session.fit_at, c, cfg["seed"], ids_by_slice)
     assert session.repacks == exp["repacks"]
+    assert session.repacks_with_slice == exp["with_slice"]
     assert torch.equal(index.bucket_indptr.cpu().long(), exp["indptr"])
     inv = index.inverse_positions().cpu().long()
     assert torch.equal(inv, exp["inverse"])
@@ -285,7 +288,7 @@ def test_token_order_repacks_when_a_cluster_outgrows_its_reservation():
         assert torch.equal(packed[0, inv[h], h], inp.k[:, h])
         assert torch.equal(packed[1, inv[h], h], inp.v[:, h])
         assert torch.equal(posting[h, inv[h]], torch.arange(cfg["tokens"]))
-    print(f"repacks: {session.repacks}")
+    print(f"repacks: {session.repacks} ({session.repacks_with_slice} counting the slice)")
 
 
 def test_decode_after_a_token_order_prefill():
