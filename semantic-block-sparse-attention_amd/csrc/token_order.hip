@@ -25,150 +25,149 @@ namespace {
 // normalize, all in fp32; descriptors with every element zero are skipped and
 // the first of equal maxima wins (torch.argmax).
 //
-// Block: 256 threads, 64 keys.  The unit keys stay in LDS in fp32 for the
-// whole block; the descriptors stream through LDS 64 at a time in bf16.  A
-// thread tells a dead descriptor from the words it multiplies (no shared
-// flag, so nothing is cleared while another thread may still read it).
-// Thread t owns keys (t & 15) + 16 i and descriptors (t >> 4) + 16 j of a
-// tile, i, j < 4: the key tile's row stride D + 4 puts the 16 rows a wave
-// reads on distinct banks.
-constexpr int NC_KEYS = 64;
-constexpr int NC_CENTS = 64;
+// The fp32 products run on bf16 MFMA: a unit key is split into three bf16
+// terms s2 = hi + mid + lo (each the rounding of what the earlier terms leave,
+// so the sum carries s2's 24 significant bits), the descriptors are bf16
+// already, every term's product is exact in fp32 and the three MFMAs
+// accumulate in fp32.
+//
+// Block: 4 waves, 16 keys per wave held in registers as MFMA A operands
+// (row lane % 16, k = 32 s + 8 (lane / 16) .. +8: the four lanes of a row
+// hold a quarter of it each); descriptors are staged through LDS 64 at a time.
+// A lane tells a dead descriptor from the words it multiplies, OR-ed over the
+// four lanes of its column.
+constexpr int NC_WAVE_KEYS = 16;
+constexpr int NC_KEYS = 4 * NC_WAVE_KEYS;   // keys per block
+constexpr int NC_CENTS = 64;                // descriptors per LDS tile
 
-template <int D>
-constexpr size_t nearest_lds_bytes() {
-  return (size_t)NC_KEYS * (D + 4) * 4 + (size_t)NC_CENTS * (D + 8) * 2 + 2 * 16 * NC_KEYS * 4;
+__device__ __forceinline__ u32x4_t pack8_bf16(const float* v) {
+  return u32x4_t{pack2bf(v[0], v[1]), pack2bf(v[2], v[3]), pack2bf(v[4], v[5]), pack2bf(v[6], v[7])};
 }
 
 template <int D>
 __global__ __launch_bounds__(256) void nearest_cluster_kernel(
     const bf16_t* __restrict__ k, int64_t n, int64_t s_tok, int64_t s_head, int router_pass,
     const bf16_t* __restrict__ codebooks, int num_clusters, int32_t* __restrict__ ids) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem_nc[];
-  constexpr int XS = D + 4;
-  constexpr int CS = D + 8;
-  constexpr int PER = D / 64;
-  float* xs = reinterpret_cast<float*>(smem_nc);                     // [64][XS]
-  bf16_t* cs = reinterpret_cast<bf16_t*>(xs + NC_KEYS * XS);         // [64][CS]
-  float* bv = reinterpret_cast<float*>(cs + NC_CENTS * CS);          // [16][64]
-  int* bi = reinterpret_cast<int*>(bv + 16 * NC_KEYS);               // [16][64]
-
+  constexpr int KS = D / 32;
+  constexpr int LDR = D + 8;
+  __shared__ __attribute__((aligned(16))) bf16_t sc[NC_CENTS * LDR];
   const int h = blockIdx.y;
-  const int64_t key0 = (int64_t)blockIdx.x * NC_KEYS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t key = (int64_t)blockIdx.x * NC_KEYS + wave * NC_WAVE_KEYS + (lane & 15);
+  const bool ok = key < n;
 
-  // unit keys, one wave per row
-  for (int r = wave; r < NC_KEYS; r += 4) {
-    const int64_t row = key0 + r;
-    float v[PER];
+  // this lane's quarter of its key row, in fp32
+  float v[KS][8];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    u32x4_t w = u32x4_t{0, 0, 0, 0};
+    if (ok)
+      w = *reinterpret_cast<const u32x4_t*>(k + key * s_tok + (int64_t)h * s_head + s * 32 + (lane >> 4) * 8);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[s][2 * j] = __uint_as_float(ww[j] << 16);
+      v[s][2 * j + 1] = __uint_as_float(ww[j] & 0xffff0000u);
+    }
+  }
+  auto row_norm = [&]() {
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      v[i] = row < n ? bf2f(k[row * s_tok + (int64_t)h * s_head + lane + 64 * i]) : 0.f;
-      ss += v[i] * v[i];
-    }
-    if (router_pass) {
-      const float n0 = fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
-      ss = 0.f;
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        v[i] = round_bf16(v[i] / n0);
-        ss += v[i] * v[i];
-      }
-    }
-    const float n1 = fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
-    ss = 0.f;
+      for (int e = 0; e < 8; ++e) ss += v[s][e] * v[s][e];
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    return fmaxf(sqrtf(ss), 1e-12f);
+  };
+  if (router_pass) {
+    const float n0 = row_norm();
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      v[i] = v[i] / n1;
-      ss += v[i] * v[i];
-    }
-    const float n2 = fmaxf(sqrtf(wave_sum(ss)), 1e-12f);
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-    for (int i = 0; i < PER; ++i) xs[r * XS + lane + 64 * i] = v[i] / n2;
+      for (int e = 0; e < 8; ++e) v[s][e] = round_bf16(v[s][e] / n0);
+  }
+  const float n1 = row_norm();
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[s][e] = v[s][e] / n1;
+  const float n2 = row_norm();
+  u32x4_t a_hi[KS], a_mid[KS], a_lo[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    float hi[8], mid[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = v[s][e] / n2;
+      hi[e] = round_bf16(x);
+      mid[e] = round_bf16(x - hi[e]);
+      lo[e] = round_bf16((x - hi[e]) - mid[e]);
+    }
+    a_hi[s] = pack8_bf16(hi);
+    a_mid[s] = pack8_bf16(mid);
+    a_lo[s] = pack8_bf16(lo);
   }
 
-  const int kg = threadIdx.x & 15, cg = threadIdx.x >> 4;
   float best[4];
-  int besti[4];
+  int bidx[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     best[i] = -INFINITY;
-    besti[i] = 0;
+    bidx[i] = 0;
   }
   const bf16_t* cb = codebooks + (int64_t)h * 2 * num_clusters * (D / 2);
-  constexpr int CHUNKS = D / 8;          // 16-byte chunks of one descriptor
+  constexpr int CHUNKS = D / 8;
   for (int c0 = 0; c0 < num_clusters; c0 += NC_CENTS) {
-    __syncthreads();                     // previous tile consumed, keys ready
+    __syncthreads();                    // the previous tile is consumed
     for (int e = threadIdx.x; e < NC_CENTS * CHUNKS; e += 256) {
       const int c = e / CHUNKS, q = e - c * CHUNKS;
       const int half = q / (CHUNKS / 2), off = (q - half * (CHUNKS / 2)) * 8;
-      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(
+      *reinterpret_cast<u32x4_t*>(&sc[c * LDR + q * 8]) = *reinterpret_cast<const u32x4_t*>(
           cb + ((int64_t)half * num_clusters + c0 + c) * (D / 2) + off);
-      *reinterpret_cast<u32x4_t*>(cs + c * CS + q * 8) = w;
     }
     __syncthreads();
-    float acc[4][4];
-    uint32_t nz[4] = {0, 0, 0, 0};       // any nonzero element of descriptor j (sign bits ignored)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int cbk = 0; cbk < NC_CENTS / 16; ++cbk) {
+      f32x4_t acc = f32x4_t{0, 0, 0, 0};
+      uint32_t nz = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-    for (int d = 0; d < D; d += 4) {
-      f32x4_t a[4];
+      for (int s = 0; s < KS; ++s) {
+        const u32x4_t b = *reinterpret_cast<const u32x4_t*>(&sc[(cbk * 16 + (lane & 15)) * LDR + s * 32 + (lane >> 4) * 8]);
+        nz |= (b.x | b.y | b.z | b.w) & 0x7fff7fffu;
+        acc = mfma16x16x32(as_bf16x8(a_hi[s]), as_bf16x8(b), acc);
+        acc = mfma16x16x32(as_bf16x8(a_mid[s]), as_bf16x8(b), acc);
+        acc = mfma16x16x32(as_bf16x8(a_lo[s]), as_bf16x8(b), acc);
+      }
+      nz |= (uint32_t)__shfl_xor((int)nz, 16, 64);
+      nz |= (uint32_t)__shfl_xor((int)nz, 32, 64);
+      if (nz) {
+        const int col = c0 + cbk * 16 + (lane & 15);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const f32x4_t*>(xs + (kg + 16 * i) * XS + d);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const u32x2_t w = *reinterpret_cast<const u32x2_t*>(cs + (cg + 16 * j) * CS + d);
-        nz[j] |= (w.x | w.y) & 0x7fff7fffu;
-        const float b0 = __uint_as_float(w.x << 16), b1 = __uint_as_float(w.x & 0xffff0000u);
-        const float b2 = __uint_as_float(w.y << 16), b3 = __uint_as_float(w.y & 0xffff0000u);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float s = acc[i][j];
-          s = fmaf(a[i].x, b0, s);
-          s = fmaf(a[i].y, b1, s);
-          s = fmaf(a[i].z, b2, s);
-          s = fmaf(a[i].w, b3, s);
-          acc[i][j] = s;
-        }
+        for (int i = 0; i < 4; ++i)
+          if (acc[i] > best[i]) {        // columns rise with cbk and c0: strict > keeps the first
+            best[i] = acc[i];
+            bidx[i] = col;
+          }
       }
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (!nz[j]) continue;
-      const int c = c0 + cg + 16 * j;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (acc[i][j] > best[i]) {
-          best[i] = acc[i][j];
-          besti[i] = c;
-        }
-    }
   }
+  // acc[i] is key row 4 (lane / 16) + i of the wave, column lane % 16: reduce the 16 columns
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    bv[cg * NC_KEYS + kg + 16 * i] = best[i];
-    bi[cg * NC_KEYS + kg + 16 * i] = besti[i];
-  }
-  __syncthreads();
-  if (threadIdx.x < NC_KEYS) {
-    const int key = threadIdx.x;
-    float b = -INFINITY;
-    int id = 0;
-    bool any = false;
-    for (int g = 0; g < 16; ++g) {
-      const float v = bv[g * NC_KEYS + key];
-      const int c = bi[g * NC_KEYS + key];
-      if (v == -INFINITY) continue;
-      if (!any || v > b || (v == b && c < id)) {
-        b = v;
-        id = c;
-        any = true;
+    float bv = best[i];
+    int bi = bidx[i];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
       }
     }
-    if (key0 + key < n) ids[(int64_t)h * n + key0 + key] = id;
+    const int64_t r = (int64_t)blockIdx.x * NC_KEYS + wave * NC_WAVE_KEYS + (lane >> 4) * 4 + i;
+    if ((lane & 15) == 0 && r < n) ids[(int64_t)h * n + r] = bi;
   }
 }
 
@@ -205,29 +204,40 @@ __global__ __launch_bounds__(1024) void append_rows_kernel(
   const uint64_t below = (1ull << lane) - 1;
 
   for (int pass = 0; pass < 2; ++pass) {
-    for (int64_t p0 = lo; p0 < hi; p0 += 64) {
-      const int64_t p = p0 + lane;
-      int id = p < hi ? id_h[p] : -1;
-      const bool bad = p < hi && (id < 0 || id >= C);
-      if (bad) {
-        id = -1;
-        if (pass == 1) rows[(int64_t)h * n + p] = -1;
-        else atomicOr(&s_flag, 2);
+    // up to 8 chunks of 64 ids are loaded together, then grouped chunk by chunk
+    for (int64_t g0 = lo; g0 < hi; g0 += 8 * 64) {
+      int idv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t p = g0 + j * 64 + lane;
+        idv[j] = p < hi ? id_h[p] : -1;
       }
-      bool pending = id >= 0;
-      for (;;) {
-        const uint64_t act = __ballot(pending);
-        if (!act) break;
-        const int lead = __ffsll((unsigned long long)act) - 1;
-        const int lid = __shfl(id, lead, 64);
-        const bool hit = pending && id == lid;
-        const uint64_t m = __ballot(hit);
-        const int start = pass ? base[lid] + mine[lid] : 0;
-        if (hit) {
-          if (pass) rows[(int64_t)h * n + p] = start + __popcll(m & below);
-          pending = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (g0 + j * 64 >= hi) break;
+        const int64_t p = g0 + j * 64 + lane;
+        int id = idv[j];
+        const bool bad = p < hi && (id < 0 || id >= C);
+        if (bad) {
+          id = -1;
+          if (pass == 1) rows[(int64_t)h * n + p] = -1;
+          else atomicOr(&s_flag, 2);
         }
-        if (lane == lead) mine[lid] += __popcll(m);
+        bool pending = id >= 0;
+        for (;;) {
+          const uint64_t act = __ballot(pending);
+          if (!act) break;
+          const int lead = __ffsll((unsigned long long)act) - 1;
+          const int lid = __shfl(id, lead, 64);
+          const bool hit = pending && id == lid;
+          const uint64_t m = __ballot(hit);
+          const int start = pass ? base[lid] + mine[lid] : 0;
+          if (hit) {
+            if (pass) rows[(int64_t)h * n + p] = start + __popcll(m & below);
+            pending = false;
+          }
+          if (lane == lead) mine[lid] += __popcll(m);
+        }
       }
     }
     __syncthreads();
@@ -398,26 +408,18 @@ int sbsa_nearest_cluster(const void* k, int64_t n, int64_t stride_tok, int64_t s
                          int num_clusters, int32_t* ids, hipStream_t stream) {
   if (!k || !codebooks || !ids || n < 0 || num_kv_heads < 1) return SBSA_ERR_ARG;
   if (num_clusters < NC_CENTS || num_clusters % NC_CENTS || num_clusters > 1024) return SBSA_ERR_UNSUPPORTED;
-  if (!aligned16(codebooks)) return SBSA_ERR_ARG;
+  if (!aligned16(codebooks) || !aligned16(k) || stride_tok % 8 || stride_head % 8) return SBSA_ERR_ARG;
   if (n == 0) return SBSA_OK;
   const dim3 grid((unsigned)((n + NC_KEYS - 1) / NC_KEYS), (unsigned)num_kv_heads);
   switch (dim) {
-    case 128: {
-      const size_t lds = nearest_lds_bytes<128>();
-      hipFuncSetAttribute((const void*)nearest_cluster_kernel<128>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      hipLaunchKernelGGL(nearest_cluster_kernel<128>, grid, dim3(256), lds, stream, (const bf16_t*)k, n,
+    case 128:
+      hipLaunchKernelGGL(nearest_cluster_kernel<128>, grid, dim3(256), 0, stream, (const bf16_t*)k, n,
                          stride_tok, stride_head, router_pass, (const bf16_t*)codebooks, num_clusters, ids);
       break;
-    }
-    case 256: {
-      const size_t lds = nearest_lds_bytes<256>();
-      hipFuncSetAttribute((const void*)nearest_cluster_kernel<256>,
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      hipLaunchKernelGGL(nearest_cluster_kernel<256>, grid, dim3(256), lds, stream, (const bf16_t*)k, n,
+    case 256:
+      hipLaunchKernelGGL(nearest_cluster_kernel<256>, grid, dim3(256), 0, stream, (const bf16_t*)k, n,
                          stride_tok, stride_head, router_pass, (const bf16_t*)codebooks, num_clusters, ids);
       break;
-    }
     default:
       return SBSA_ERR_UNSUPPORTED;
   }
