@@ -63,6 +63,20 @@ __device__ __forceinline__ const bf16_t* uniform_ptr(const bf16_t* p) {
   return (const bf16_t*)(((uint64_t)hi << 32) | lo);
 }
 
+// One 16-byte-per-lane buffer load straight into LDS (lane l writes bytes
+// 16 l .. 16 l + 15 past lds_addr).  Issued from inline assembly so that the
+// compiler does not track it: it would otherwise make every later LDS read
+// wait for the load (it cannot tell that the read is from another buffer).
+// The kernel waits for these loads itself (s_waitcnt vmcnt) before the
+// barrier that publishes a tile.  M0 holds the LDS base, as the instruction
+// requires; nothing else in the kernel uses M0.
+__device__ __forceinline__ void lds_dma16(u32x4_t rsrc, uint32_t lds_addr, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -135,8 +149,8 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
                 8 * (i16 & 1);
 
   // LDS: K tiles in buffers 0/1, V tiles in buffers 2/3
-  unsigned char* const kbuf[2] = {smem_attn, smem_attn + S::TILE_BYTES};
-  unsigned char* const vbuf[2] = {smem_attn + 2 * S::TILE_BYTES, smem_attn + 3 * S::TILE_BYTES};
+  auto kbuf_at = [&](int i) { return smem_attn + i * S::TILE_BYTES; };
+  auto vbuf_at = [&](int i) { return smem_attn + (2 + i) * S::TILE_BYTES; };
 
   // Thread 0 claims each item one item ahead: the atomic for the next item is
   // issued when an item starts and resolved when the next one does, so its
@@ -199,14 +213,19 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     auto issue = [&](const bf16_t* base, int t, unsigned char* dst_tile, bool is_k) {
       const int t0 = t * KT;
       const int valid = __builtin_amdgcn_readfirstlane((int)((uint32_t)(nkeys - t0) * rs_bytes));
-      __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)uniform_ptr(base + (int64_t)t0 * rs), (short)0, valid, BUFFER_CONFIG);
-      unsigned char* dst = dst_tile + wave * 1024;
+      const uint64_t b = (uint64_t)(base + (int64_t)t0 * rs);
+      u32x4_t rsrc;     // raw buffer resource: base, stride 0, valid bytes, config
+      rsrc.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+      rsrc.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
+      rsrc.z = (uint32_t)valid;
+      rsrc.w = (uint32_t)BUFFER_CONFIG;
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          (uint32_t)(uintptr_t)(lds_void_t*)(dst_tile + wave * 1024));
 #pragma unroll
       for (int m = 0; m < S::PER_WAVE; ++m) {
         const uint32_t roff = kvoff + (uint32_t)(m * 4 * S::ROWS_PER_INST) * rs_bytes;
         const uint32_t slot = is_k ? kslot[m & 1] : vslot;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(dst + m * 4096), 16, roff + slot, 0, 0, 0);
+        lds_dma16(rsrc, dst + m * 4096, roff + slot);
       }
     };
 
@@ -341,38 +360,54 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
 
     // One step: S(t+1) on the MFMA units while the VALU turns S(t) into
     // probabilities, then O += V(t) P(t).  K(t+2) and V(t+1) stream into the
-    // buffers that K(t) and V(t-1) left.
+    // buffers that K(t) and V(t-1) left.  Two forms: the steady one, for
+    // tiles whose successor some row of the wave still sees, is straight-line
+    // code the scheduler can interleave; the general one handles the wave's
+    // last active tile and the tiles past every row of the wave, whose loads
+    // the wave still issues for the others.
+    auto issue_next = [&](int t) {
+      if (t + 2 < ntiles) issue(kp, t + 2, kbuf_at(t & 1), true);
+      if (t + 1 < ntiles) issue(vp, t + 1, vbuf_at((t + 1) & 1), false);
+    };
+    auto finish_step = [&]() {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    };
+    auto step_full = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
+      issue_next(t);
+      mask_track(cur, t);
+      u32x4_t pb[2];
+      gemm_s_body(nxt, kbuf_at((t + 1) & 1));
+      exp_pack(cur, pb);
+      // the VALU work of exp_pack between the MFMAs of S(t+1)
+      __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
+#pragma unroll
+      for (int f = 0; f < KS - KA_AHEAD; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+#pragma unroll
+      for (int f = 0; f < KA_AHEAD; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+      gemm_pv(pb, vbuf_at(t & 1));
+      finish_step();
+    };
+    // the general form, for the tiles around a wave's last active one
     auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
-      if (t + 2 < ntiles) issue(kp, t + 2, kbuf[t & 1], true);
-      if (t + 1 < ntiles) issue(vp, t + 1, vbuf[(t + 1) & 1], false);
+      issue_next(t);
       const bool act = t * KT <= wave_lim;
       const bool act_n = t + 1 < ntiles && (t + 1) * KT <= wave_lim;
       u32x4_t pb[2];
       if (act) mask_track(cur, t);
-      if (act && act_n) {
-        gemm_s_body(nxt, kbuf[(t + 1) & 1]);
+      if (act_n) gemm_s(nxt, kbuf_at((t + 1) & 1));
+      if (act) {
         exp_pack(cur, pb);
-        // the VALU work of exp_pack between the MFMAs of S(t+1)
-        __builtin_amdgcn_sched_group_barrier(0x100, KA_AHEAD, 0);
-#pragma unroll
-        for (int f = 0; f < KS - KA_AHEAD; ++f) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        }
-#pragma unroll
-        for (int f = 0; f < KA_AHEAD; ++f) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        }
-      } else if (act) {
-        exp_pack(cur, pb);
-      } else if (act_n) {
-        gemm_s(nxt, kbuf[(t + 1) & 1]);
+        gemm_pv(pb, vbuf_at(t & 1));
       }
-      if (act) gemm_pv(pb, vbuf[t & 1]);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
+      finish_step();
     };
 
     // Each row's probabilities are taken against a reference maximum fixed
@@ -381,9 +416,9 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     // restarts the item with the rows' true maxima as reference.
     bool forced = false;
     for (int pass = 0; pass < 2; ++pass) {
-      issue(kp, 0, kbuf[0], true);
-      issue(vp, 0, vbuf[0], false);
-      if (ntiles > 1) issue(kp, 1, kbuf[1], true);
+      issue(kp, 0, kbuf_at(0), true);
+      issue(vp, 0, vbuf_at(0), false);
+      if (ntiles > 1) issue(kp, 1, kbuf_at(1), true);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -393,7 +428,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       f32x16_t sA, sB;
-      gemm_s(sA, kbuf[0]);
+      gemm_s(sA, kbuf_at(0));
       mask_track(sA, 0);
       if (!forced) {
         // reference maximum: the row's maximum over the first tile (key 0 of
@@ -401,7 +436,15 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
-      for (int t = 0; t < ntiles; t += 2) {
+      // tiles 0..t_last hold keys some row of this wave may see; the steady
+      // loop runs while the next tile is active too
+      const int t_last = min(ntiles - 1, wave_lim / KT);
+      int t = 0;
+      for (; t + 2 <= t_last; t += 2) {
+        step_full(t, sA, sB);
+        step_full(t + 1, sB, sA);
+      }
+      for (; t < ntiles; t += 2) {
         step(t, sA, sB);
         if (t + 1 < ntiles) step(t + 1, sB, sA);
       }
@@ -461,10 +504,35 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
 }
 
 
-// S6: per (query, KV head), one wave.  Seeds with the local window, then
-// folds the query's cluster partials in cluster order (query-major order of
-// the reference's entries).  Each lane owns E = G*D/64 consecutive values of
+// S6: per (query, KV head), one wave.  The reference folds the query's
+// partials into the window's result one cluster at a time (online
+// log-sum-exp, cluster order).  Here the wave first lists the query's entries
+// (lanes test 64 clusters at once), takes the maximum of all the LSEs, and then
+// sums exp(lse - max)-weighted partials with four entries' loads in flight, so
+// no load waits on the previous fold.  The result is the same merge, rounded
+// once instead of per step.  Each lane owns E = G*D/64 consecutive values of
 // one head.
+constexpr int COMBINE_MAX_LIST = 1024;   // entries per (query, head): at most C
+
+template <int E>
+__device__ __forceinline__ void load_bf16_row(const bf16_t* src, float (&v)[E]) {
+  if constexpr (E % 8 == 0) {
+#pragma unroll
+    for (int k = 0; k < E / 8; ++k) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(src + 8 * k);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[8 * k + 2 * t] = __uint_as_float(ww[t] << 16);
+        v[8 * k + 2 * t + 1] = __uint_as_float(ww[t] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = bf2f(src[e]);
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(256) void combine_kernel(
     const int32_t* __restrict__ qmask, const int32_t* __restrict__ nvis,
@@ -475,47 +543,92 @@ __global__ __launch_bounds__(256) void combine_kernel(
     float* __restrict__ out_lse, int Qc, int Hkv, int C) {
   constexpr int E = G * D / 64;
   static_assert(E >= 1 && D % E == 0, "lane share");
-  const int lane = threadIdx.x & 63;
-  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ int s_list[4][COMBINE_MAX_LIST];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
   if (gw >= (int64_t)Qc * Hkv) return;
   const int qi = (int)(gw / Hkv), h = (int)(gw % Hkv);
   const int j = (lane * E) / D, d0 = (lane * E) % D;
   const int Hq = Hkv * G;
-  float acc[E];
-  float m = local_lse[(int64_t)qi * Hq + h * G + j];
-  {
-    const bf16_t* src = local_o + (int64_t)qi * lo_sq + (int64_t)(h * G + j) * lo_sh + d0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = bf2f(src[e]);
-  }
-  float den = 1.f;
-  const int W = C / 32;
-  const int32_t* qm = qmask + ((int64_t)qi * Hkv + h) * W;
+  int* list = s_list[wave];
+
+  // the query's entries, in cluster order
+  const int32_t* qm = qmask + ((int64_t)qi * Hkv + h) * (C / 32);
   const int32_t* qr = qrank + ((int64_t)qi * Hkv + h) * C;
-  for (int w = 0; w < W; ++w) {
-    uint32_t bits = (uint32_t)qm[w];
-    while (bits) {
-      const int b = __builtin_ctz(bits);
-      bits &= bits - 1;
-      const int c = w * 32 + b;
-      if (nvis[h * C + c] <= 0) continue;
-      const int64_t entry = (int64_t)rev_indptr[h * C + c] + qr[c];
-      const float le = part_lse[entry * G + j];
-      const float nm = fmaxf(m, le);
-      const float sc = expf(m - nm);
-      const float wt = expf(le - nm);
-      const bf16_t* src = part_o + (entry * G + j) * D + d0;
+  const uint64_t below = (1ull << lane) - 1;
+  int n = 0;
+  for (int c0 = 0; c0 < C; c0 += 64) {
+    const int c = c0 + lane;
+    bool sel = false;
+    int entry = 0;
+    if (c < C && (((uint32_t)qm[c >> 5] >> (c & 31)) & 1u) && nvis[h * C + c] > 0) {
+      sel = true;
+      entry = rev_indptr[h * C + c] + qr[c];
+    }
+    const uint64_t m = __ballot(sel);
+    if (sel) list[n + __popcll(m & below)] = entry;
+    n += __popcll(m);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // the largest LSE: the window's and every partial's
+  const float lse_w = local_lse[(int64_t)qi * Hq + h * G + j];
+  float mx = lse_w;
+  for (int k = 0; k < n; k += 4) {
+    float l4[4];
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = acc[e] * sc + bf2f(src[e]) * wt;
-      den = den * sc + wt;
-      m = nm;
+    for (int u = 0; u < 4; ++u) l4[u] = k + u < n ? part_lse[(int64_t)list[k + u] * G + j] : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mx = fmaxf(mx, l4[u]);
+  }
+
+  float acc[E];
+  float den;
+  {
+    float v[E];
+    load_bf16_row<E>(local_o + (int64_t)qi * lo_sq + (int64_t)(h * G + j) * lo_sh + d0, v);
+    den = expf(lse_w - mx);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = v[e] * den;
+  }
+  for (int k = 0; k < n; k += 4) {
+    float v[4][E], wt[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool ok = k + u < n;
+      const int64_t entry = ok ? list[k + u] : 0;
+      wt[u] = ok ? part_lse[entry * G + j] : -INFINITY;
+      if (ok) load_bf16_row<E>(part_o + (entry * G + j) * D + d0, v[u]);
+      else
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[u][e] = 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float w = expf(wt[u] - mx);
+      den += w;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = fmaf(v[u][e], w, acc[e]);
     }
   }
   const float inv = 1.0f / fmaxf(den, 1e-30f);
   bf16_t* dst = out + (int64_t)qi * out_sq + (int64_t)(h * G + j) * out_sh + d0;
+  if constexpr (E % 8 == 0) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) dst[e] = f2bf(acc[e] * inv);
-  if (out_lse && (lane * E) % D == 0) out_lse[(int64_t)qi * Hq + h * G + j] = m + logf(den);
+    for (int k = 0; k < E / 8; ++k) {
+      u32x4_t w;
+      w.x = pack2bf(acc[8 * k + 0] * inv, acc[8 * k + 1] * inv);
+      w.y = pack2bf(acc[8 * k + 2] * inv, acc[8 * k + 3] * inv);
+      w.z = pack2bf(acc[8 * k + 4] * inv, acc[8 * k + 5] * inv);
+      w.w = pack2bf(acc[8 * k + 6] * inv, acc[8 * k + 7] * inv);
+      *reinterpret_cast<u32x4_t*>(dst + 8 * k) = w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) dst[e] = f2bf(acc[e] * inv);
+  }
+  if (out_lse && (lane * E) % D == 0) out_lse[(int64_t)qi * Hq + h * G + j] = mx + logf(den);
 }
 
 template <int D, int G>
@@ -643,6 +756,7 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
                          int num_clusters, hipStream_t stream) {
   if (!qmask || !nvis || !rev_indptr || !qrank || !local_o || !local_lse || !out) return SBSA_ERR_ARG;
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_clusters % 32) return SBSA_ERR_ARG;
+  if (num_clusters > COMBINE_MAX_LIST) return SBSA_ERR_UNSUPPORTED;
   if (num_queries == 0) return SBSA_OK;
   int rc = combine_dispatch(dim, num_q_heads / num_kv_heads, qmask, nvis, rev_indptr, qrank,
                             (const bf16_t*)part_o, part_lse, (const bf16_t*)local_o, lo_sq, lo_sh,
