@@ -302,6 +302,18 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         lmax_all = fmaxf(lmax_all, fmaxf(fmaxf(sacc[e], sacc[e + 1]), fmaxf(sacc[e + 2], sacc[e + 3])));
     };
 
+    // the masking alone, for the passes that do not track the maximum
+    auto mask_only = [&](f32x16_t& sacc, int t) {
+      const int t0 = t * KT;
+      if (t0 + KT > nkeys || t0 + KT - 1 > wave_min) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = t0 + 8 * (e >> 2) + 4 * g + (e & 3);
+          if (!(key < nkeys && key <= qlim)) sacc[e] = NEG_INF;
+        }
+      }
+    };
+
     // probabilities exp2(s - m) of a tile against the row's reference maximum
     // as the B operands of the two 16-key steps of O^T
     float m_ref = 0.f, l_part = 0.f;
@@ -375,7 +387,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     };
     auto step_full = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
       issue_next(t);
-      mask_track(cur, t);
+      mask_only(cur, t);
       u32x4_t pb[2];
       gemm_s_body(nxt, kbuf_at((t + 1) & 1));
       exp_pack(cur, pb);
@@ -395,15 +407,19 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       gemm_pv(pb, vbuf_at(t & 1));
       finish_step();
     };
-    // the general form, for the tiles around a wave's last active one
-    auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
+    // the general form, for the tiles around a wave's last active one; with
+    // sweep set it only tracks the rows' maxima (no probabilities, no O)
+    auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt, bool sweep) {
       issue_next(t);
       const bool act = t * KT <= wave_lim;
       const bool act_n = t + 1 < ntiles && (t + 1) * KT <= wave_lim;
       u32x4_t pb[2];
-      if (act) mask_track(cur, t);
-      if (act_n) gemm_s(nxt, kbuf_at((t + 1) & 1));
       if (act) {
+        if (sweep) mask_track(cur, t);
+        else mask_only(cur, t);
+      }
+      if (act_n) gemm_s(nxt, kbuf_at((t + 1) & 1));
+      if (act && !sweep) {
         exp_pack(cur, pb);
         gemm_pv(pb, vbuf_at(t & 1));
       }
@@ -411,11 +427,13 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     };
 
     // Each row's probabilities are taken against a reference maximum fixed
-    // from the first tile; no accumulator is rescaled in the loop.  A key
-    // more than OVERFLOW_LOG2 above the reference (probabilities past 2^64)
-    // restarts the item with the rows' true maxima as reference.
-    bool forced = false;
-    for (int pass = 0; pass < 2; ++pass) {
+    // from the first tile; no accumulator is rescaled in the loop.  If a row's
+    // sum of probabilities passes 2^OVERFLOW_LOG2 (which any probability past
+    // that bound would cause; a probability up to it is safe in fp32 and
+    // bf16), the item is redone: a sweep over the tiles finds the rows' true
+    // maxima, and the last pass takes them as reference.
+    for (int pass = 0; pass < 3; ++pass) {
+      const bool sweep = pass == 1;
       issue(kp, 0, kbuf_at(0), true);
       issue(vp, 0, vbuf_at(0), false);
       if (ntiles > 1) issue(kp, 1, kbuf_at(1), true);
@@ -430,31 +448,34 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       f32x16_t sA, sB;
       gemm_s(sA, kbuf_at(0));
       mask_track(sA, 0);
-      if (!forced) {
+      if (pass == 0) {
         // reference maximum: the row's maximum over the first tile (key 0 of
         // an item is visible to every row, so it is finite)
         const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
-      // tiles 0..t_last hold keys some row of this wave may see; the steady
-      // loop runs while the next tile is active too
-      const int t_last = min(ntiles - 1, wave_lim / KT);
       int t = 0;
-      for (; t + 2 <= t_last; t += 2) {
-        step_full(t, sA, sB);
-        step_full(t + 1, sB, sA);
+      if (!sweep) {
+        // tiles 0..t_last hold keys some row of this wave may see; the steady
+        // loop runs while the next tile is active too
+        const int t_last = min(ntiles - 1, wave_lim / KT);
+        for (; t + 2 <= t_last; t += 2) {
+          step_full(t, sA, sB);
+          step_full(t + 1, sB, sA);
+        }
       }
       for (; t < ntiles; t += 2) {
-        step(t, sA, sB);
-        if (t + 1 < ntiles) step(t + 1, sB, sA);
+        step(t, sA, sB, sweep);
+        if (t + 1 < ntiles) step(t + 1, sB, sA, sweep);
       }
-      // the row's true maximum; restart if any exceeds its reference by too much
-      float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
-      mx = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
-      const bool over = mx > m_ref + OVERFLOW_LOG2;
-      if (forced || !__syncthreads_or(over ? 1 : 0)) break;
-      m_ref = mx;
-      forced = true;
+      if (pass == 0) {
+        const float l = l_part + __shfl_xor(l_part, 32, 64);
+        const bool over = !(l <= __builtin_exp2f(OVERFLOW_LOG2));
+        if (!__syncthreads_or(over ? 1 : 0)) break;
+      } else if (sweep) {
+        const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
+        m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
+      }
     }
 
     // epilogue: normalise, then write the partial (or the local window) and

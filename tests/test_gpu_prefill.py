@@ -146,3 +146,27 @@ def test_layer_prefill_chunk_loop_through_the_operator():
         err = (g - want).abs() - (2e-2 + 1e-2 * want.abs())
         bad_q = (err > 0).flatten(1).any(-1)
         assert int(bad_q.sum()) <= 2, f"chunk {cs}: {int(bad_q.sum())} queries off"
+
+
+@pytest.mark.parametrize("beta", [3.0, 6.0])
+def test_dense_chunk_redone_when_a_key_towers_over_the_first_tile(beta):
+    """A key far above every score of the first tile: probabilities against the
+    first tile's maximum pass 2^64 (beta 3: about 2^90) or fp32 range (beta 6), the
+    item is redone with the rows' true maxima, and the result is exact attention."""
+    from semblo_amd.kv_outer import dense_causal_attention
+    gen = torch.Generator().manual_seed(17)
+    length, hq, hkv, d = 2048, 8, 2, 128
+    cs, ce = 1024, 1535
+    u = torch.randn(d, generator=gen)
+    q = (3 * u + torch.randn(length, hq, d, generator=gen)).to(torch.bfloat16)
+    k = torch.randn(length, hkv, d, generator=gen)
+    v = torch.randn(length, hkv, d, generator=gen).to(torch.bfloat16)
+    k[900] = beta * u                                      # tile 28 of the keys, every query sees it
+    k = k.to(torch.bfloat16)
+    out = dense_causal_attention(q[cs:ce + 1].to(DEV), k.to(DEV), v.to(DEV), sm_scale=d ** -0.5,
+                                 chunk_start=cs).cpu()
+    p = torch.arange(cs, ce + 1)
+    keys = (torch.arange(length)[None, :] <= p[:, None])[:, None, :].expand(-1, hkv, -1)
+    want = attention_reference(q[cs:ce + 1], keys, k, v, d ** -0.5)
+    err = assert_close_bf16(out, want, f"towering key, beta {beta}")
+    print(f"beta {beta}: max err {err:.3g}")
