@@ -198,41 +198,69 @@ __global__ __launch_bounds__(256) void kmeans_assign_kernel(
 }
 
 // Per-cluster fp32 sums of the member rows, in row order (deterministic).
-// One block per cluster walks the assignment in 256-row chunks, compacts the
-// members of the chunk in order, and each thread accumulates its dimensions.
+// One block per cluster takes the assignment in chunks of 4096 rows: each
+// wave compacts the members of its 1024 contiguous rows into its own list
+// (ballots, no block barrier), the four lists form the chunk's members in row
+// order, and each thread adds its dimensions of those rows in that order with
+// eight rows' loads in flight.
+constexpr int KU_CHUNK = 4096;
+
 __global__ __launch_bounds__(256) void kmeans_update_kernel(
     const float* __restrict__ x, int64_t ld_x, const int32_t* __restrict__ row_index, int64_t n,
     const int32_t* __restrict__ assign, int dim, float* __restrict__ sums,
     int32_t* __restrict__ counts) {
-  __shared__ int members[256];
+  __shared__ int members[KU_CHUNK];        // source rows, wave w's at [w * 1024, ...)
   __shared__ int wave_cnt[4];
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const uint64_t below = (1ull << lane) - 1;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims threadIdx.x + 256*j, dim <= 1024
   int total = 0;
-  for (int64_t base = 0; base < n; base += 256) {
-    int64_t i = base + threadIdx.x;
-    bool mine = i < n && assign[i] == c;
-    uint64_t ball = __ballot(mine);
-    int before = __popcll(ball & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-    if (lane == 0) wave_cnt[wave] = __popcll(ball);
-    __syncthreads();
-    int off = 0;
-    for (int w = 0; w < wave; ++w) off += wave_cnt[w];
-    int cnt = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-    if (mine) members[off + before] = (int)(i - base);
-    __syncthreads();
-    for (int m = 0; m < cnt; ++m) {
-      int64_t r = base + members[m];
-      int64_t src = row_index ? (int64_t)row_index[r] : r;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int d = threadIdx.x + 256 * j;
-        if (d < dim) acc[j] += x[src * ld_x + d];
-      }
+  for (int64_t base = 0; base < n; base += KU_CHUNK) {
+    const int64_t seg = base + wave * (KU_CHUNK / 4);
+    int cnt_w = 0;
+#pragma unroll 4
+    for (int k = 0; k < KU_CHUNK / 4 / 64; ++k) {
+      const int64_t i = seg + k * 64 + lane;
+      const bool mine = i < n && assign[i] == c;
+      const uint64_t ball = __ballot(mine);
+      if (mine) members[wave * (KU_CHUNK / 4) + cnt_w + __popcll(ball & below)] =
+          row_index ? row_index[i] : (int)i;
+      cnt_w += __popcll(ball);
     }
-    total += cnt;
+    if (lane == 0) wave_cnt[wave] = cnt_w;
+    __syncthreads();
+    for (int w = 0; w < 4; ++w) {
+      const int* lst = members + w * (KU_CHUNK / 4);
+      const int cnt = wave_cnt[w];
+      int m = 0;
+      for (; m + 8 <= cnt; m += 8) {
+        float v[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t src = lst[m + u];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int d = threadIdx.x + 256 * j;
+            v[u][j] = d < dim ? x[src * ld_x + d] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] += v[u][j];
+      }
+      for (; m < cnt; ++m) {
+        const int64_t src = lst[m];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = threadIdx.x + 256 * j;
+          if (d < dim) acc[j] += x[src * ld_x + d];
+        }
+      }
+      total += cnt;
+    }
     __syncthreads();
   }
 #pragma unroll
@@ -446,6 +474,109 @@ __global__ void pack_kv_kernel(const bf16_t* __restrict__ key, const bf16_t* __r
   }
 }
 
+// Vectorised forms of the two kernels above for rows of 64..512 elements with
+// 16-byte-aligned rows: each lane owns 8 consecutive elements (one 16-byte
+// load), LPR = dim / 8 lanes hold a row, and a norm is reduced over the
+// lanes of its row (or of its factor's part).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v, int group) {
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1)
+    if (o < group) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(u32x4_t w, float (&v)[8]) {
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = __uint_as_float(ww[j] << 16);
+    v[2 * j + 1] = __uint_as_float(ww[j] & 0xffff0000u);
+  }
+}
+
+template <int LPR>
+__global__ __launch_bounds__(256) void route_vectors_vec_kernel(const bf16_t* __restrict__ x, int64_t rows,
+                                                                int64_t ld_x, int factors,
+                                                                bf16_t* __restrict__ out, int64_t ld_out) {
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int sub = lane % LPR;
+  const int group = LPR / factors;            // lanes of one factor's part
+  const bool ok = row < rows;
+  float v[8];
+  unpack8(ok ? *reinterpret_cast<const u32x4_t*>(x + row * ld_x + sub * 8) : u32x4_t{0, 0, 0, 0}, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+  const float n1 = fmaxf(sqrtf(row_sum<LPR>(ss, group)), 1e-12f);
+  float ss2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v[e] = round_bf16(v[e] / n1);
+    ss2 += v[e] * v[e];
+  }
+  const float n2 = fmaxf(sqrtf(row_sum<LPR>(ss2, group)), 1e-12f);
+  if (ok) {
+    u32x4_t w;
+    w.x = pack2bf(v[0] / n2, v[1] / n2);
+    w.y = pack2bf(v[2] / n2, v[3] / n2);
+    w.z = pack2bf(v[4] / n2, v[5] / n2);
+    w.w = pack2bf(v[6] / n2, v[7] / n2);
+    *reinterpret_cast<u32x4_t*>(out + row * ld_out + sub * 8) = w;
+  }
+}
+
+template <int LPR>
+__global__ __launch_bounds__(256) void key_space_vec_kernel(const bf16_t* __restrict__ k, int64_t length,
+                                                            int64_t ld_k, int router_pass,
+                                                            float* __restrict__ space_f32,
+                                                            bf16_t* __restrict__ space_bf16) {
+  constexpr int RPW = 64 / LPR;
+  constexpr int D = LPR * 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int sub = lane % LPR;
+  const bool ok = row < length;
+  float v[8];
+  unpack8(ok ? *reinterpret_cast<const u32x4_t*>(k + row * ld_k + sub * 8) : u32x4_t{0, 0, 0, 0}, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+  if (router_pass) {
+    const float n0 = fmaxf(sqrtf(row_sum<LPR>(ss, LPR)), 1e-12f);
+    ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = round_bf16(v[e] / n0);
+      ss += v[e] * v[e];
+    }
+  }
+  const float n1 = fmaxf(sqrtf(row_sum<LPR>(ss, LPR)), 1e-12f);
+  ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    v[e] = v[e] / n1;
+    ss += v[e] * v[e];
+  }
+  const float n2 = fmaxf(sqrtf(row_sum<LPR>(ss, LPR)), 1e-12f);
+  if (ok) {
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = v[e] / n2;
+    float* df = space_f32 + row * D + sub * 8;
+    *reinterpret_cast<f32x4_t*>(df) = f32x4_t{s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4_t*>(df + 4) = f32x4_t{s[4], s[5], s[6], s[7]};
+    *reinterpret_cast<u32x4_t*>(space_bf16 + row * D + sub * 8) =
+        u32x4_t{pack2bf(s[0], s[1]), pack2bf(s[2], s[3]), pack2bf(s[4], s[5]), pack2bf(s[6], s[7])};
+  }
+}
+
+bool vec_rows_ok(const void* p, int64_t ld, int dim) {
+  return ((uintptr_t)p & 15) == 0 && ld % 8 == 0 && (dim == 64 || dim == 128 || dim == 256 || dim == 512);
+}
+
 }  // namespace
 
 extern "C" {
@@ -455,6 +586,20 @@ int sbsa_route_vectors(const void* x, int64_t rows, int64_t ld_x, int dim, int f
   if (!x || !out || rows < 0 || factors < 1 || dim % factors || dim / factors > 512 || dim < 1)
     return SBSA_ERR_ARG;
   if (rows == 0) return SBSA_OK;
+  const int lpr = dim / 8;
+  if (vec_rows_ok(x, ld_x, dim) && vec_rows_ok(out, ld_out, dim) && lpr % factors == 0 &&
+      (dim / factors) % 8 == 0) {
+    const int64_t per_block = 4 * (64 / lpr);
+    const dim3 grid((unsigned)((rows + per_block - 1) / per_block));
+    switch (lpr) {
+      case 8: hipLaunchKernelGGL(route_vectors_vec_kernel<8>, grid, dim3(256), 0, stream, (const bf16_t*)x, rows, ld_x, factors, (bf16_t*)out, ld_out); break;
+      case 16: hipLaunchKernelGGL(route_vectors_vec_kernel<16>, grid, dim3(256), 0, stream, (const bf16_t*)x, rows, ld_x, factors, (bf16_t*)out, ld_out); break;
+      case 32: hipLaunchKernelGGL(route_vectors_vec_kernel<32>, grid, dim3(256), 0, stream, (const bf16_t*)x, rows, ld_x, factors, (bf16_t*)out, ld_out); break;
+      default: hipLaunchKernelGGL(route_vectors_vec_kernel<64>, grid, dim3(256), 0, stream, (const bf16_t*)x, rows, ld_x, factors, (bf16_t*)out, ld_out); break;
+    }
+    SBSA_CHECK_LAUNCH();
+    return SBSA_OK;
+  }
   int blocks = (int)((rows + 3) / 4);
   hipLaunchKernelGGL(route_vectors_kernel, dim3(blocks), dim3(256), 0, stream,
                      (const bf16_t*)x, rows, ld_x, dim, factors, (bf16_t*)out, ld_out);
@@ -466,6 +611,19 @@ int sbsa_key_space(const void* k, int64_t length, int64_t ld_k, int dim, int rou
                    float* space_f32, void* space_bf16, hipStream_t stream) {
   if (!k || !space_f32 || !space_bf16 || length < 0 || dim < 1 || dim > 512) return SBSA_ERR_ARG;
   if (length == 0) return SBSA_OK;
+  if (vec_rows_ok(k, ld_k, dim) && ((uintptr_t)space_f32 & 15) == 0 && ((uintptr_t)space_bf16 & 15) == 0) {
+    const int lpr = dim / 8;
+    const int64_t per_block = 4 * (64 / lpr);
+    const dim3 grid((unsigned)((length + per_block - 1) / per_block));
+    switch (lpr) {
+      case 8: hipLaunchKernelGGL(key_space_vec_kernel<8>, grid, dim3(256), 0, stream, (const bf16_t*)k, length, ld_k, router_pass, space_f32, (bf16_t*)space_bf16); break;
+      case 16: hipLaunchKernelGGL(key_space_vec_kernel<16>, grid, dim3(256), 0, stream, (const bf16_t*)k, length, ld_k, router_pass, space_f32, (bf16_t*)space_bf16); break;
+      case 32: hipLaunchKernelGGL(key_space_vec_kernel<32>, grid, dim3(256), 0, stream, (const bf16_t*)k, length, ld_k, router_pass, space_f32, (bf16_t*)space_bf16); break;
+      default: hipLaunchKernelGGL(key_space_vec_kernel<64>, grid, dim3(256), 0, stream, (const bf16_t*)k, length, ld_k, router_pass, space_f32, (bf16_t*)space_bf16); break;
+    }
+    SBSA_CHECK_LAUNCH();
+    return SBSA_OK;
+  }
   hipLaunchKernelGGL(key_space_kernel, dim3((unsigned)((length + 3) / 4)), dim3(256), 0, stream,
                      (const bf16_t*)k, length, ld_k, dim, router_pass, space_f32,
                      (bf16_t*)space_bf16);
