@@ -84,20 +84,23 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
   }
   __syncthreads();
 
-  // per row: lse over C, then w = exp(s - lse + logmix) in place
+  // per row: lse over C, then w = exp(s - lse + logmix) in place (base-2
+  // hardware exp/log: about 1 ulp, far below the selection's near-tie margin)
+  constexpr float LOG2E = 1.4426950408889634f;
   for (int r = wave; r < R; r += 4) {
     float* row = ssc + r * LDS_C;
     float m = -INFINITY;
     for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     float l = 0.f;
-    for (int c = lane; c < C; c += 64) l += expf(row[c] - m);
-    l = wave_sum(l);
-    float lse = m + logf(l);
+    for (int c = lane; c < C; c += 64) l += __builtin_amdgcn_exp2f((row[c] - m) * LOG2E);
+    l = wave_sum_dpp(l);
     int q = q0 + r / G, t = r % G;
     float lm = 0.f;
     if (a.logmix && q < a.Q) lm = a.logmix[(int64_t)q * a.Hq + h * G + t];
-    for (int c = lane; c < C; c += 64) row[c] = expf(row[c] - lse + lm);
+    // log2 of exp(lm) / (sum exp(s))
+    const float off2 = (lm - m) * LOG2E - __builtin_amdgcn_logf(l);
+    for (int c = lane; c < C; c += 64) row[c] = __builtin_amdgcn_exp2f(__builtin_fmaf(row[c], LOG2E, off2));
   }
   __syncthreads();
 
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
     float real_size[16];
     const int nk = C / 64;
     float hi = -INFINITY, lo = INFINITY;
-    long long live_total = 0;
+    int live_total = 0;      // token counts: sizes sum to at most the prompt length
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       score[k] = NEG;
@@ -129,43 +132,63 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
         real_size[k] = rs;
         size[k] = s;
         bool live = s > 0.f;
-        float sc = logf(fmaxf(p, 1e-38f));
-        if (a.beta != 0.f) sc = sc - a.beta * logf(1.0f + s);
+        constexpr float LN2 = 0.69314718055994531f;
+        float sc = __builtin_amdgcn_logf(fmaxf(p, 1e-38f)) * LN2;
+        if (a.beta != 0.f) sc = sc - a.beta * (__builtin_amdgcn_logf(1.0f + s) * LN2);
         sc = live ? sc : NEG;
         score[k] = sc;
         hi = fmaxf(hi, sc);
         lo = fminf(lo, live ? sc : POS);
-        if (live) live_total += (long long)s;
+        if (live) live_total += (int)s;
       }
     }
-    hi = wave_max(hi) + 1e-6f;
-    lo = wave_min(lo) - 1e-6f;
+    hi = wave_max_dpp(hi) + 1e-6f;
+    lo = wave_min_dpp(lo) - 1e-6f;
     lo = fminf(lo, hi - 1e-5f);
-    live_total = wave_sum_i64(live_total);
+    live_total = wave_sum_i32_dpp(live_total);
     float budget = a.target;
     if (a.sink > 0) budget = fmaxf(a.target - (float)a.sink, 0.f);
     const bool all_fit = (float)live_total < budget;
-    for (int it = 0; it < a.iters; ++it) {
-      float mid = (lo + hi) * 0.5f;
-      long long above = 0;
+    // two bisection steps per round: the first step's mid and both possible
+    // second mids are counted together (the same fp32 mids as one step at a time)
+    for (int it = 0; it < a.iters; it += 2) {
+      const float m0 = (lo + hi) * 0.5f;
+      const float m1 = (m0 + hi) * 0.5f;     // second mid if m0 reaches the budget
+      const float m2 = (lo + m0) * 0.5f;     // second mid otherwise
+      int c0 = 0, c1 = 0, c2 = 0;
 #pragma unroll
       for (int k = 0; k < 16; ++k)
-        if (k < nk && score[k] >= mid) above += (long long)size[k];
-      above = wave_sum_i64(above);
-      bool reach = (float)above >= budget;
-      lo = reach ? mid : lo;
-      hi = reach ? hi : mid;
+        if (k < nk) {
+          const int sk = (int)size[k];
+          c0 += score[k] >= m0 ? sk : 0;
+          c1 += score[k] >= m1 ? sk : 0;
+          c2 += score[k] >= m2 ? sk : 0;
+        }
+      wave_sum3_i32_dpp(c0, c1, c2);
+      if ((float)c0 >= budget) {
+        lo = m0;
+        if (it + 1 < a.iters) {
+          if ((float)c1 >= budget) lo = m1;
+          else hi = m1;
+        }
+      } else {
+        hi = m0;
+        if (it + 1 < a.iters) {
+          if ((float)c2 >= budget) lo = m2;
+          else hi = m2;
+        }
+      }
     }
     const float theta = all_fit ? NEG : lo;
     int nsel = 0;
-    long long ntok = 0;
+    int ntok = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k < nk) {
         int c = lane + 64 * k;
         bool sel = (size[k] > 0.f && score[k] >= theta) || (a.sink > 0 && c == 0 && real_size[k] > 0.f);
         nsel += sel ? 1 : 0;
-        ntok += sel ? (long long)real_size[k] : 0;
+        ntok += sel ? (int)real_size[k] : 0;
         uint64_t ball = __ballot(sel);
         if (lane < 2) {
           uint32_t word = (uint32_t)(ball >> (32 * lane));
@@ -175,8 +198,8 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
         }
       }
     }
-    nsel = wave_sum_i32(nsel);
-    ntok = wave_sum_i64(ntok);
+    nsel = wave_sum_i32_dpp(nsel);
+    ntok = wave_sum_i32_dpp(ntok);
     if (lane == 0) {
       if (a.counts) a.counts[(int64_t)q * a.Hkv + h] = nsel;
       if (a.tokens) a.tokens[(int64_t)q * a.Hkv + h] = (int32_t)ntok;
