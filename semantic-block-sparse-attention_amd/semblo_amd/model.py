@@ -24,6 +24,7 @@ from .attention_op import register_layer
 from .config import SembloRuntimeConfig
 from .fused_decode import fused_decode_step
 from .fused_prefill import CausalSnapshot, fused_chunk_attention
+from .kv_outer import dense_causal_attention
 from .state import ProductPostingIndex
 from .trivial_router import trivial_router_vectors
 
@@ -78,6 +79,14 @@ class SembloAttention:
         index.original_kv = (k_post, v)
         return index
 
+    def _build_stream(self, device) -> torch.cuda.Stream:
+        """The stream the index is built on while the dense chunks run (default priority)."""
+        st = getattr(self, "_side_stream", None)
+        if st is None or st.device != torch.device(device):
+            st = torch.cuda.Stream(device=device)
+            self._side_stream = st
+        return st
+
     def begin_token_outer_prefill(self, tokens: int, chunk: int, **kw):
         """A token-order prefill session of ``tokens`` positions in slices of ``chunk``
         (the reference's layer.begin_token_outer_prefill, streamed_prefill.py:563-564)."""
@@ -124,15 +133,42 @@ class SembloAttention:
         kk = k_post.view(length, self.num_kv_heads, self.head_dim)
         vv = v.view(length, self.num_kv_heads, self.head_dim)
         out = output.view(length, self.num_heads, self.head_dim)
-        index = self._ingest_prompt_kv(kp, kk, vv)
-        self.index = index
         self.target_tokens = cfg.budget(length)
-        snapshot = CausalSnapshot(index)
         step = cfg.query_chunk_size
-        for start in range(0, length, step):
+        cap = cfg.dense_prefix_x * self.target_tokens
+        # The dense-prefix chunks read only the prompt-order K/V, not the index:
+        # they are enqueued first on this stream, and the index is built on a
+        # second stream (default priority) that waits only for the inputs, so
+        # the build's host work (its random draws and host reads) overlaps the
+        # dense attention.  The sparse chunks wait for the build.  The outputs
+        # do not depend on the order.
+        main = torch.cuda.current_stream(q.device)
+        inputs_ready = torch.cuda.Event()
+        inputs_ready.record(main)
+        for start in range(0, min(length, cap + 1), step):
             end = min(length, start + step)
-            cap = cfg.dense_prefix_x * self.target_tokens
-            qs = None if start <= cap else self._query_state(qp[start:end])
+            if timing is not None:
+                n = end - start
+                timing.add_flops(4.0 * self.head_dim * self.num_heads * (n * (start + 1) + n * (n - 1) // 2))
+            dense_causal_attention(q[start:end], kk, vv, sm_scale=self.scaling, chunk_start=start,
+                                   out=out[start:end], timing=timing)
+        side = self._build_stream(q.device)
+        side.wait_event(inputs_ready)
+        with torch.cuda.stream(side):
+            index = self._ingest_prompt_kv(kp, kk, vv)
+            built = torch.cuda.Event()
+            built.record(side)
+        main.wait_event(built)
+        for t in (index.codebooks, index.posting_positions, index.bucket_indptr, index.bucket_sizes,
+                  index._inverse_positions, index.packed_kv):
+            t.record_stream(main)
+        self.index = index
+        snapshot = CausalSnapshot(index)
+        for start in range(0, length, step):
+            if start <= cap:
+                continue
+            end = min(length, start + step)
+            qs = self._query_state(qp[start:end])
             fused_chunk_attention(
                 q[start:end], qs, index, None, snapshot, start, end - 1,
                 temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,

@@ -14,9 +14,11 @@ The random draws (the fit sample, the initial centroids and the restart rows
 of empty clusters) come from a CPU ``torch.Generator`` seeded with
 ``codebook_seed``, in the reference's call order.  The reference draws on the
 keys' device; drawing on the CPU makes the partition independent of the
-device's RNG, and identical to the reference's own CPU build.  It costs one
-small host read of the cluster counts per k-means iteration, as the
-reference's ``empty.any()`` test does.
+device's RNG, and identical to the reference's own CPU build.  The
+reference reads the cluster counts every k-means iteration (its
+``empty.any()`` test); here the iterations run ahead and one read finds the
+first iteration that left a cluster empty, which is redone from there with
+the restart rows drawn, so the result is the same with fewer host reads.
 """
 from __future__ import annotations
 
@@ -120,8 +122,11 @@ class ProductPostingIndex:
         space_bf = torch.empty(length, index_dim, dtype=torch.bfloat16, device=dev)
         cent_f32 = torch.empty(c, index_dim, dtype=torch.float32, device=dev)
         cent_bf = torch.empty(c, index_dim, dtype=torch.bfloat16, device=dev)
-        sums = torch.empty(c, index_dim, dtype=torch.float32, device=dev)
-        counts = torch.empty(c, dtype=torch.int32, device=dev)
+        n_it = max(iters, 1)
+        sums_hist = torch.empty(n_it, c, index_dim, dtype=torch.float32, device=dev)
+        counts_hist = torch.empty(n_it, c, dtype=torch.int32, device=dev)
+        counts_host = torch.empty(n_it, c, dtype=torch.int32, pin_memory=True)
+        no_restart = torch.full((c,), -1, dtype=torch.int32, device=dev)
         assign_s = torch.empty(fit_n, dtype=torch.int32, device=dev)
         assign_all = torch.empty(length, dtype=torch.int32, device=dev)
         cap = length + c * (max(align, 1) - 1)
@@ -133,37 +138,57 @@ class ProductPostingIndex:
         codebooks = torch.empty(hkv, 2, c, index_dim // 2, dtype=product_keys.dtype, device=dev)
         ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        counts_host = torch.empty(c, dtype=torch.int32, pin_memory=True)
 
-        for h in range(hkv):
-            kh = pk[:, h]
-            _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
-                      int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
-            # fit_flat_codebook: sample, init, iterations (flat_index.py:237-288)
+        def draw_sample_and_init():
+            # fit_flat_codebook's first two draws (flat_index.py:237-262)
             perm = torch.randperm(length, generator=gen)
-            sample_idx = perm[:fit_n].to(torch.int32).to(dev, non_blocking=False)
+            sample = perm[:fit_n].to(torch.int32).to(dev)
             init = torch.randperm(fit_n, generator=gen)[:c].to(torch.int32).to(dev)
-            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(space_f32),
-                      index_dim, _lib.ptr(sample_idx), c, index_dim, _lib.ptr(cent_f32),
-                      _lib.ptr(cent_bf), s)
-            for _ in range(iters):
+            return sample, init
+
+        def iterate(start, sample_idx):
+            # k-means steps start.. with no restart rows; an iteration that left a
+            # cluster empty is found afterwards from counts_hist and redone
+            for it in range(start, iters):
                 _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, _lib.ptr(sample_idx),
                           fit_n, _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_s), s)
                 _lib.call("sbsa_kmeans_update", _lib.ptr(space_f32), index_dim,
                           _lib.ptr(sample_idx), fit_n, _lib.ptr(assign_s), c, index_dim,
-                          _lib.ptr(sums), _lib.ptr(counts), s)
-                counts_host.copy_(counts)          # one host read per iteration
-                torch.cuda.current_stream(dev).synchronize()
-                empty = counts_host == 0
+                          _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]), s)
+                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
+                          _lib.ptr(no_restart), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
+                          c, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+
+        def first_empty(it0):
+            """The first iteration >= it0 that left a cluster empty, or -1 (one host read)."""
+            counts_host[it0:iters].copy_(counts_hist[it0:iters])
+            torch.cuda.current_stream(dev).synchronize()
+            hit = torch.nonzero((counts_host[it0:iters] == 0).any(dim=1)).flatten()
+            return it0 + int(hit[0]) if hit.numel() else -1
+
+        draws = draw_sample_and_init()
+        for h in range(hkv):
+            kh = pk[:, h]
+            _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
+                      int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
+            sample_idx, init = draws
+            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(space_f32),
+                      index_dim, _lib.ptr(sample_idx), c, index_dim, _lib.ptr(cent_f32),
+                      _lib.ptr(cent_bf), s)
+            iterate(0, sample_idx)
+            it = first_empty(0) if iters > 0 else -1
+            while it >= 0:
+                # the reference's restart of the empty clusters at iteration it
+                # (flat_index.py:277-283), then the later iterations again
+                empty = counts_host[it] == 0
                 src = torch.full((c,), -1, dtype=torch.int32)
-                n_empty = int(empty.sum())
-                if n_empty:
-                    repl = torch.randperm(fit_n, generator=gen)[:n_empty]
-                    src[empty] = repl.to(torch.int32)
+                src[empty] = torch.randperm(fit_n, generator=gen)[:int(empty.sum())].to(torch.int32)
                 src_d = src.to(dev)
-                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums), _lib.ptr(counts),
+                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
                           _lib.ptr(src_d), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
                           c, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+                iterate(it + 1, sample_idx)
+                it = first_empty(it + 1) if it + 1 < iters else -1
             # assign every key, lay the runs out, descriptor
             _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, None, length,
                       _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_all), s)
@@ -172,6 +197,9 @@ class ProductPostingIndex:
                       _lib.ptr(inverse[h]), _lib.ptr(totals[h:h + 1]), _lib.ptr(ws), ws_bytes, s)
             _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
                       c, index_dim, None, _lib.ptr(codebooks[h]), s)
+            if h + 1 < hkv:
+                # the next head's draws, on the host while the GPU lays this head out
+                draws = draw_sample_and_init()
         width = int(totals.max().item())
         posting = posting_full[:, :width].contiguous()
         return cls(codebooks=codebooks, posting_positions=posting, bucket_indptr=indptr,

@@ -130,3 +130,30 @@ def test_causal_sizes_match_the_snapshot_rule():
         want = ref.causal_sizes_at(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(),
                                    idx.bucket_sizes.cpu(), limit)
         assert torch.equal(got, want)
+
+
+def test_build_with_empty_clusters_matches_the_oracle():
+    """Heads 0 and 2 draw their keys from a few directions, so k-means leaves
+    clusters empty and restarts them on sample rows drawn from the generator;
+    head 1 is ordinary.  The restart draws, and the draws of every later head,
+    must follow the reference's order (flat_index.py:277-283)."""
+    gen = torch.Generator().manual_seed(23)
+    length, d = 2048, 128
+    k = torch.randn(length, 3, d, generator=gen)
+    for h in (0, 2):
+        dirs = torch.randn(6, d, generator=gen)
+        k[:, h] = dirs[torch.randint(0, 6, (length,), generator=gen)] \
+            + 1e-3 * torch.randn(length, d, generator=gen)
+    product = ref.routing_normalize_keys(k.to(torch.bfloat16))
+    traces = []
+    want = ref.build_flat_index(product, codebook_seed=5, traces=traces)
+    empties = [sum(len(x[1]) for x in tr if x[0] == "empty") for tr in traces]
+    assert empties[0] > 0 and empties[1] == 0 and empties[2] > 0, empties
+    idx = _build_gpu(product, codebook_seed=5)
+    _check_index_invariants(idx, length)
+    got_m = _membership(idx.posting_positions.cpu(), idx.bucket_indptr.cpu(), idx.bucket_sizes.cpu())
+    want_m = _membership(want["posting"], want["indptr"], want["sizes"])
+    moved, gap = membership_near_ties(product, want["codebooks"], got_m, want_m)
+    print(f"restart draws per head {empties}: {moved} keys moved (near-ties, widest {gap:.2f} ulps)")
+    assert moved <= max(2, got_m.numel() // 200)
+    assert (idx.codebooks.cpu().float() - want["codebooks"].float()).abs().max() < 2e-2
