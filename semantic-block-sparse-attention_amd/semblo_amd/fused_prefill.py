@@ -2,7 +2,9 @@
 semblo/vllm_plugin/fused_prefill.py seams, paper path: FA3 page 16, KV-outer).
 
   CausalSnapshot          cluster sizes at a position       (fused_prefill.py:44-135)
-  fused_chunk_attention   dense prefix or select + KV-outer (fused_prefill.py:219-482)
+  fused_chunk_attention   dense prefix or select + KV-outer (fused_prefill.py:219-482),
+                          also as its two halves: fused_chunk_plan (selection and
+                          reverse index) and fused_chunk_execute (the attention)
   fused_decode_attention  one query over the packed prompt  (fused_prefill.py:625-718)
 """
 from __future__ import annotations
@@ -13,7 +15,7 @@ import torch
 
 from . import _lib
 from .fused_select import theta_select_bitmask_flat
-from .kv_outer import dense_causal_attention, kv_outer_attention
+from .kv_outer import dense_causal_attention, kv_outer_execute, kv_outer_plan
 
 
 @dataclass(frozen=True)
@@ -48,6 +50,85 @@ class CausalSnapshot:
         return self.sizes
 
 
+class ChunkPlan:
+    """The selection side of one sparse chunk: its causal snapshot, the per-query
+    cluster masks and the reverse index, all on the device."""
+
+    def __init__(self, chunk_start, chunk_end, wstart, causal_sizes, tokens, kv):
+        self.chunk_start, self.chunk_end, self.wstart = chunk_start, chunk_end, wstart
+        self.causal_sizes, self.tokens, self.kv = causal_sizes, tokens, kv
+
+    def tensors(self):
+        kv = self.kv
+        return (self.causal_sizes, self.tokens, kv.qmask, kv.nvis, kv.qvals, kv.counts,
+                kv.rev_indptr, kv.nnz_d, kv.qrank)
+
+
+def chunk_window_start(chunk_start: int, target_tokens: int, dense_prefix_x: int = 4,
+                       local: int = 0) -> int:
+    """0 for a dense-prefix chunk (chunk_start <= x * K), else the window's first
+    position (fused_prefill.py:259-279)."""
+    cap = dense_prefix_x * target_tokens
+    return 0 if chunk_start <= cap else max(0, chunk_start - local)
+
+
+def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, chunk_start: int,
+                     chunk_end: int, *, temperature: float, beta: float, target_tokens: int,
+                     queries_per_block: int = 32, iters: int = 16, local: int = 0,
+                     dense_prefix_x: int = 4) -> ChunkPlan:
+    """Selection and reverse index of a sparse chunk (fused_prefill.py:281-482 up to
+    the attention calls); no host read."""
+    q_count = q_chunk.shape[0]
+    hkv = index.num_kv_heads
+    c = index.num_buckets
+    wstart = chunk_window_start(chunk_start, target_tokens, dense_prefix_x, local)
+    if wstart == 0:
+        raise ValueError("a dense-prefix chunk has no selection to plan")
+    sizes = snapshot_state.advance(wstart - 1)
+    causal_sizes = sizes.clone()
+    vectors = query_state.vectors[0]
+    logmix = query_state.mixture_weights[0].float().clamp_min(1e-12).log()
+    g_union = min(queries_per_block, q_count)
+    nb = (q_count + g_union - 1) // g_union
+    bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
+    qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
+    _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None],
+                                          bitmask, temperature=temperature, beta=beta,
+                                          target_tokens=target_tokens, g_union=g_union,
+                                          iters=iters, qmask=qmask)
+    kv = kv_outer_plan(qmask, causal_sizes, num_queries=q_count)
+    return ChunkPlan(chunk_start, chunk_end, wstart, causal_sizes, tokens, kv)
+
+
+def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int, *, sm_scale: float,
+                        fa3_page_size: int = 16, out: torch.Tensor | None = None, timing=None,
+                        window_kv=None) -> torch.Tensor:
+    """The attention of a planned sparse chunk, given its partial count ``nnz``."""
+    q_count, hq, d = q_chunk.shape
+    hkv = index.num_kv_heads
+    wstart, chunk_start, chunk_end = plan.wstart, plan.chunk_start, plan.chunk_end
+    if timing is not None:
+        # selected rows of every (query, KV head), each read by its G query heads,
+        # plus the causal window (p - chunk_start + 1 keys per query and head)
+        g = hq // hkv
+        window = q_count * (q_count + 1) // 2
+        timing.add_flops(4.0 * d * (g * plan.tokens.to(torch.float64).sum() + hq * window))
+    if window_kv is not None:
+        if window_kv[0].shape[0] != chunk_end + 1 - wstart:
+            raise ValueError("window_kv must hold positions wstart..chunk_end")
+        window = window_kv
+    else:
+        if index.original_kv is None:
+            raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
+                               "(index.original_kv), which this index no longer holds")
+        k_orig, v_orig = index.original_kv
+        window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
+    res, _ = kv_outer_execute(q_chunk, index.packed_kv, plan.kv, nnz, index.bucket_indptr,
+                              sm_scale=sm_scale, local_kv=window, chunk_start=chunk_start,
+                              wstart=wstart, out=out, timing=timing)
+    return res
+
+
 def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor,
                           snapshot_state: CausalSnapshot, chunk_start: int, chunk_end: int, *,
                           temperature: float, beta: float, target_tokens: int,
@@ -63,21 +144,18 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     chunk's own tokens through the exact causal window.  ``window_kv`` (k, v),
     rows wstart..chunk_end in prompt order, replaces the slice of
     ``index.original_kv`` for that window (the token-order prefill, whose
-    store has no prompt-order copy).
+    store has no prompt-order copy).  One host read (the partial count).
     """
     if not kv_outer_default or not fa3_page_size:
         raise NotImplementedError("only the paper path (FA3 page body, KV-outer) is built")
     q_count = q_chunk.shape[0]
-    hkv = index.num_kv_heads
-    c = index.num_buckets
-    cap = dense_prefix_x * target_tokens
-    wstart = 0 if chunk_start <= cap else max(0, chunk_start - local)
-    if index.original_kv is None and (wstart == 0 or window_kv is None):
-        raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
-                           "(index.original_kv), which this index no longer holds")
-    hq, d = q_chunk.shape[1], q_chunk.shape[2]
+    wstart = chunk_window_start(chunk_start, target_tokens, dense_prefix_x, local)
     if wstart == 0:
+        if index.original_kv is None:
+            raise RuntimeError("the prefill reads the chunk's window from the prompt-order K/V "
+                               "(index.original_kv), which this index no longer holds")
         k_orig, v_orig = index.original_kv
+        hq, d = q_chunk.shape[1], q_chunk.shape[2]
         if timing is not None:
             # sum over p in the chunk of (p + 1) keys, every query head, 4 D FLOPs per key
             n = q_count
@@ -85,36 +163,14 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
             timing.add_flops(4.0 * d * hq * keys)
         return dense_causal_attention(q_chunk, k_orig, v_orig, sm_scale=sm_scale,
                                       chunk_start=chunk_start, out=out, timing=timing)
-    sizes = snapshot_state.advance(wstart - 1)
-    causal_sizes = sizes.clone()
-    vectors = query_state.vectors[0]
-    logmix = query_state.mixture_weights[0].float().clamp_min(1e-12).log()
-    g_union = min(queries_per_block, q_count)
-    nb = (q_count + g_union - 1) // g_union
-    bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
-    qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
-    _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None],
-                                          bitmask, temperature=temperature, beta=beta,
-                                          target_tokens=target_tokens, g_union=g_union,
-                                          iters=iters, qmask=qmask)
-    if timing is not None:
-        # selected rows of every (query, KV head), each read by its G query heads,
-        # plus the causal window (p - chunk_start + 1 keys per query and head)
-        g = hq // hkv
-        window = q_count * (q_count + 1) // 2
-        timing.add_flops(4.0 * d * (g * tokens.to(torch.float64).sum() + hq * window))
-    if window_kv is not None:
-        if window_kv[0].shape[0] != chunk_end + 1 - wstart:
-            raise ValueError("window_kv must hold positions wstart..chunk_end")
-        window = window_kv
-    else:
-        k_orig, v_orig = index.original_kv
-        window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
-    res, _ = kv_outer_attention(q_chunk, index.packed_kv, qmask, causal_sizes,
-                                index.bucket_indptr, sm_scale=sm_scale, page_size=fa3_page_size,
-                                aligned=True, local_kv=window, chunk_start=chunk_start,
-                                wstart=wstart, out=out, timing=timing)
-    return res
+    plan = fused_chunk_plan(q_chunk, query_state, index, snapshot_state, chunk_start, chunk_end,
+                            temperature=temperature, beta=beta, target_tokens=target_tokens,
+                            queries_per_block=queries_per_block, iters=iters, local=local,
+                            dense_prefix_x=dense_prefix_x)
+    nnz = int(plan.kv.nnz_d.item())               # the one host read of the chunk
+    return fused_chunk_execute(plan, q_chunk, index, nnz, sm_scale=sm_scale,
+                               fa3_page_size=fa3_page_size, out=out, timing=timing,
+                               window_kv=window_kv)
 
 
 def fused_decode_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor, *,

@@ -86,10 +86,44 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
         raise ValueError("the local window must run from wstart to the chunk's last query")
     if k_loc.stride() != v_loc.stride():
         raise ValueError("the window's K and V must share a layout")
+    plan = kv_outer_plan(qmask, causal_sizes, num_queries=qn)
+    nnz = int(plan.nnz_d.item())                  # the one host read of the chunk
+    return kv_outer_execute(q, packed_kv, plan, nnz, bucket_indptr, sm_scale=sm_scale,
+                            local_kv=local_kv, chunk_start=chunk_start, wstart=wstart, out=out,
+                            want_stats=want_stats, grid=grid, timing=timing)
+
+
+class KVOuterPlan:
+    """The reverse index of one chunk (kv_outer.py:254-329): everything the
+    attention needs from the selection, built before the one host read."""
+
+    def __init__(self, qmask, nvis, qvals, counts, rev_indptr, nnz_d, qrank):
+        self.qmask, self.nvis, self.qvals, self.counts = qmask, nvis, qvals, counts
+        self.rev_indptr, self.nnz_d, self.qrank = rev_indptr, nnz_d, qrank
+
+
+def kv_outer_plan(qmask: torch.Tensor, causal_sizes: torch.Tensor, *, num_queries: int) -> KVOuterPlan:
+    """The reverse index of a chunk's selection (no host read)."""
     nvis = causal_sizes if causal_sizes.dtype == torch.int32 else causal_sizes.to(torch.int32)
     nvis = nvis.contiguous()
-    qvals, counts, rev_indptr, nnz_d, qrank = build_reverse_index(qmask, nvis, num_queries=qn)
-    nnz = int(nnz_d.item())                       # the one host read of the chunk
+    qvals, counts, rev_indptr, nnz_d, qrank = build_reverse_index(qmask, nvis, num_queries=num_queries)
+    return KVOuterPlan(qmask, nvis, qvals, counts, rev_indptr, nnz_d, qrank)
+
+
+def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan, nnz: int,
+                     bucket_indptr: torch.Tensor, *, sm_scale: float, local_kv, chunk_start: int,
+                     wstart: int, out: torch.Tensor | None = None, want_stats: bool = False,
+                     grid: int | None = None, timing=None):
+    """The work list, the attention and the combine of one chunk, given its plan and
+    its partial count ``nnz`` (read on the host)."""
+    qn, hq, d = q.shape
+    hkv = packed_kv.shape[2]
+    g = hq // hkv
+    qmask, nvis, qvals, counts = plan.qmask, plan.nvis, plan.qvals, plan.counts
+    rev_indptr, qrank = plan.rev_indptr, plan.qrank
+    c = qmask.shape[2] * 32
+    dev = q.device
+    k_loc, v_loc = local_kv
     part_o = torch.empty(max(nnz, 1), g, d, dtype=q.dtype, device=dev)
     part_lse = torch.empty(max(nnz, 1), g, dtype=torch.float32, device=dev)
     local_o = torch.empty_like(q)

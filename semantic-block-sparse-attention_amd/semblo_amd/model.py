@@ -23,7 +23,7 @@ from .arena import DecodeArena
 from .attention_op import register_layer
 from .config import SembloRuntimeConfig
 from .fused_decode import fused_decode_step
-from .fused_prefill import CausalSnapshot, fused_chunk_attention
+from .fused_prefill import CausalSnapshot, fused_chunk_execute, fused_chunk_plan
 from .kv_outer import dense_causal_attention
 from .state import ProductPostingIndex
 from .trivial_router import trivial_router_vectors
@@ -154,26 +154,31 @@ class SembloAttention:
                                    out=out[start:end], timing=timing)
         side = self._build_stream(q.device)
         side.wait_event(inputs_ready)
+        sparse = [(st, min(length, st + step)) for st in range(0, length, step) if st > cap]
         with torch.cuda.stream(side):
             index = self._ingest_prompt_kv(kp, kk, vv)
-            built = torch.cuda.Event()
-            built.record(side)
-        main.wait_event(built)
+            snapshot = CausalSnapshot(index)
+            # every sparse chunk's selection and reverse index, then one host read
+            # of all their partial counts (in place of one read per chunk)
+            plans = [fused_chunk_plan(q[st:en], self._query_state(qp[st:en]), index, snapshot, st,
+                                      en - 1, temperature=cfg.selection_temperature,
+                                      beta=cfg.bucket_size_penalty, target_tokens=self.target_tokens,
+                                      iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x)
+                     for st, en in sparse]
+            nnz = torch.cat([pl.kv.nnz_d for pl in plans]).cpu().tolist() if plans else []
+            planned = torch.cuda.Event()
+            planned.record(side)
+        main.wait_event(planned)
         for t in (index.codebooks, index.posting_positions, index.bucket_indptr, index.bucket_sizes,
                   index._inverse_positions, index.packed_kv):
             t.record_stream(main)
+        for pl in plans:
+            for t in pl.tensors():
+                t.record_stream(main)
         self.index = index
-        snapshot = CausalSnapshot(index)
-        for start in range(0, length, step):
-            if start <= cap:
-                continue
-            end = min(length, start + step)
-            qs = self._query_state(qp[start:end])
-            fused_chunk_attention(
-                q[start:end], qs, index, None, snapshot, start, end - 1,
-                temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
-                target_tokens=self.target_tokens, sm_scale=self.scaling, iters=cfg.iters,
-                dense_prefix_x=cfg.dense_prefix_x, out=out[start:end], timing=timing)
+        for (st, en), pl, n in zip(sparse, plans, nnz):
+            fused_chunk_execute(pl, q[st:en], index, int(n),
+                                sm_scale=self.scaling, out=out[st:en], timing=timing)
         self.adopt_index(index)
         return output
 
