@@ -227,11 +227,16 @@ def main():
             _log(f"warm-up {i} done")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(args.steps):
+        # events between the steps only log the spread; nothing waits on them
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        marks[0].record()
+        for i in range(args.steps):
             run_prefill(layer, inp, conf)
+            marks[i + 1].record()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / max(args.steps, 1)
-        _log(f"prefill {ms:.2f} ms/layer")
+        per_step = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
+        _log(f"prefill {ms:.2f} ms/layer (steps on the GPU clock: {', '.join(f'{x:.1f}' for x in per_step)})")
         # one instrumented pass: attention kernel time and FLOPs, and the build time
         timing = KernelTiming()
         store = KernelTiming() if conf.get("order") == "token" else None

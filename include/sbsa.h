@@ -140,16 +140,21 @@ int sbsa_prefill_item_rows(void);
 /* ---- S5: KV-outer prefill attention ---------------------------------------------
  * The work list replacing the per-(cluster, KV head) FA3 varlen calls and the
  * local-window call of kv_outer_attention (semblo/vllm_plugin/kv_outer.py:661-753).
- * items are int4 {head, cluster or -1 (local window), first query slot, count},
- * grouped in one segment per XCD (the query tiles of a KV head's window, and
- * those of one cluster, share an XCD and its L2); queue (int32[24]) receives
- * the segments' sizes and offsets and zeroed counters.  queries_per_item =
- * 128 / (Hq/Hkv). */
+ * items are 32-byte records {head, cluster or -1 (local window), first query
+ * slot, count, visible rows nvis[h, c], first partial slot rev_indptr[h*C+c] +
+ * first query slot, first packed row indptr[h, c], 0}, so the attention
+ * kernel resolves an item with one load; indptr [Hkv, C+1], nvis [Hkv, C] and
+ * rev_indptr [Hkv*C + 1] are those later passed to sbsa_prefill_attend (any
+ * valid arrays when no cluster has queries).  Items are grouped in one segment
+ * per XCD (the query tiles of a KV head's window, and those of one cluster,
+ * share an XCD and its L2); queue (int32[24]) receives the segments' sizes and
+ * offsets and zeroed counters.  queries_per_item = 128 / (Hq/Hkv). */
 int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
                                  int num_clusters, int queries_per_item);
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
-                       int num_queries, int queries_per_item, int has_local, void* items,
-                       int64_t items_cap, int32_t* queue, hipStream_t stream);
+                       int num_queries, int queries_per_item, int has_local,
+                       const int32_t* indptr, const int32_t* nvis, const int32_t* rev_indptr,
+                       void* items, int64_t items_cap, int32_t* queue, hipStream_t stream);
 
 /* Attention over the work list (kv_outer.py:482-816; dense chunks:
  * fused_prefill.py:155-189).  q [Qc, Hq, dim] (strides q_sq, q_sh); packed

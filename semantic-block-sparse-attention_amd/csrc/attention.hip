@@ -12,8 +12,8 @@
 // Design (MI355X): one persistent kernel walks a work list of items.  An item
 // is (KV head, cluster or the local window, a tile of 128/G queries); its
 // 128 (query, head) rows run against the cluster's contiguous packed run (or
-// the prompt-order window, causally masked) in 64-key tiles.  Both GEMMs are
-// on bf16 MFMA 16x16x32 in the transposed form S^T = K Q^T, O^T = V^T P^T,
+// the prompt-order window, causally masked) in 32-key tiles.  Both GEMMs are
+// on bf16 MFMA 32x32x16 in the transposed form S^T = K Q^T, O^T = V^T P^T,
 // so the softmax probabilities come out of the first MFMA already in the
 // B-operand layout of the second and never pass through LDS.
 #include "sbsa_common.h"
@@ -32,7 +32,7 @@ struct AttnArgs {
   const int32_t* nvis;      // [Hkv, C] visible rows per cluster
   const int32_t* rev_indptr;// [Hkv*C + 1]
   const int32_t* qvals;     // [nnz] query slots per (head, cluster)
-  const int4* items;
+  const PrefillItem* items;
   int32_t* queue;           // n[8], offset[8], counter[8]: one work queue per XCD
   bf16_t* part_o;           // [nnz, G, D]
   float* part_lse;          // [nnz, G]
@@ -72,6 +72,14 @@ __device__ __forceinline__ const bf16_t* uniform_ptr(const bf16_t* p) {
 // requires; nothing else in the kernel uses M0.
 __device__ __forceinline__ void lds_dma16(u32x4_t rsrc, uint32_t lds_addr, uint32_t voffset) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
+// The same for one dword per lane (lane l writes bytes 4 l .. 4 l + 3).
+__device__ __forceinline__ void lds_dma4(u32x4_t rsrc, uint32_t lds_addr, uint32_t voffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                :
                : "s"(lds_addr), "v"(voffset), "s"(rsrc)
                : "memory", "m0");
@@ -152,18 +160,26 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   auto kbuf_at = [&](int i) { return smem_attn + i * S::TILE_BYTES; };
   auto vbuf_at = [&](int i) { return smem_attn + (2 + i) * S::TILE_BYTES; };
 
-  // Thread 0 claims each item one item ahead: the atomic for the next item is
-  // issued when an item starts and resolved when the next one does, so its
-  // latency hides behind the item's work.
+  // Thread 0 claims work one item ahead: the atomic for the following claim
+  // is issued when a claim resolves, so its latency hides behind an item's
+  // work.  Items are used one further ahead: when an item starts, the next
+  // one is claimed and its record is loaded, and once the item's first tiles
+  // are in, wave 0 loads the next item's query slots straight into LDS.  An
+  // item then starts with all of its addresses known, and its Q loads and
+  // first tile loads share one round trip.
+  // the queues' sizes and offsets are read once, into LDS
+  __shared__ int s_queue[16];
+  if (threadIdx.x < 16) s_queue[threadIdx.x] = a.queue[threadIdx.x];
   int pend = 0;
   if (threadIdx.x == 0) pend = atomicAdd(&a.queue[16 + home], 1);
-  for (;;) {
+  __syncthreads();
+  auto next_index = [&]() -> int {
     if (threadIdx.x == 0) {
       int claimed = -1;
       for (;;) {
         const int x = (home + probe) & 7;
-        if (pend < a.queue[x]) {
-          claimed = a.queue[8 + x] + pend;
+        if (pend < s_queue[x]) {
+          claimed = s_queue[8 + x] + pend;
           break;
         }
         if (++probe == 8) break;
@@ -173,29 +189,68 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       if (claimed >= 0) pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
     }
     __syncthreads();
-    const int idx = __builtin_amdgcn_readfirstlane(s_item);   // uniform: scalar loads below
+    const int v = __builtin_amdgcn_readfirstlane(s_item);   // uniform: scalar loads below
     __syncthreads();
-    if (idx < 0) break;
-    const int4 it = a.items[idx];
-    const int h = it.x, c = it.y, qb = it.z, qn = it.w;
+    return v;
+  };
+  // this lane's Q row R = wave*32 + l32 is (query slot R / G, head R % G)
+  const int row_i = (wave * 32 + l32) / G, row_j = (wave * 32 + l32) % G;
+  // a cluster item's query slots, qvals[entry0 ..][0 .. qn), into s_qslots
+  // (wave 0; slots past qn read as 0 and are not used)
+  __shared__ int s_qslots[PREFILL_ROWS];
+  auto fetch_slots = [&](const PrefillItem& r) {
+    const int c = __builtin_amdgcn_readfirstlane(r.c);
+    if (wave != 0 || c < 0) return;
+    const int qn = __builtin_amdgcn_readfirstlane(r.qn);
+    const uint64_t b = (uint64_t)(a.qvals + __builtin_amdgcn_readfirstlane(r.entry0));
+    u32x4_t rsrc;
+    rsrc.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    rsrc.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
+    rsrc.z = (uint32_t)qn * 4u;
+    rsrc.w = (uint32_t)BUFFER_CONFIG;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)s_qslots);
+#pragma unroll
+    for (int k = 0; k < PREFILL_ROWS / G; k += 64) lds_dma4(rsrc, dst + 4 * k, (uint32_t)(lane + k) * 4u);
+  };
+  PrefillItem rec{};
+  int idx = next_index();
+  if (idx >= 0) {
+    rec = a.items[idx];
+    fetch_slots(rec);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  int idx_n = -1;
+  for (; idx >= 0; idx = idx_n) {
+    const int h = __builtin_amdgcn_readfirstlane(rec.h), c = __builtin_amdgcn_readfirstlane(rec.c);
+    const int qb = __builtin_amdgcn_readfirstlane(rec.qb), qn = __builtin_amdgcn_readfirstlane(rec.qn);
+    const int64_t entry0 = __builtin_amdgcn_readfirstlane(rec.entry0);
+    const int64_t row0 = __builtin_amdgcn_readfirstlane(rec.row0);
     const bool local = c < 0;
+    // this lane's query (-1 past the item's queries); a cluster item's slots
+    // were loaded into LDS during the previous item
+    const int qidx_cur = row_i >= qn ? -1 : (local ? qb + row_i : s_qslots[row_i]);
+    int nkeys = local ? (int)(a.chunk_start + qb + qn - a.wstart) : __builtin_amdgcn_readfirstlane(rec.nkeys);
+    idx_n = next_index();
+    if (idx_n >= 0) rec = a.items[idx_n];
+    // once, after this item's first tiles are in (every wave has read its
+    // slot by then); the next item's first step, or its own wait, publishes it
+    bool prefetched = false;
+    auto prefetch_queries = [&]() {
+      if (idx_n >= 0 && !prefetched) fetch_slots(rec);
+      prefetched = true;
+    };
     const bf16_t* kp;
     const bf16_t* vp;
     int64_t rs;
-    int nkeys;
-    int64_t entry0 = 0;
     if (local) {
       kp = a.korig + (int64_t)h * a.o_sh;   // row 0 is position wstart
       vp = a.vorig + (int64_t)h * a.o_sh;
       rs = a.o_st;
-      nkeys = (int)(a.chunk_start + qb + qn - a.wstart);
     } else {
-      int64_t r0g = a.indptr[h * (a.C + 1) + c];
-      kp = a.packed + r0g * a.Hkv * D + (int64_t)h * D;
+      kp = a.packed + row0 * a.Hkv * D + (int64_t)h * D;
       vp = kp + a.packed_len * a.Hkv * D;
       rs = (int64_t)a.Hkv * D;
-      nkeys = a.nvis[h * a.C + c];
-      entry0 = (int64_t)a.rev_indptr[h * a.C + c] + qb;
     }
     // uniform values (scalar registers): the buffer resources built from them
     // need no per-lane loop
@@ -203,8 +258,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     vp = uniform_ptr(vp);
     rs = __builtin_amdgcn_readfirstlane((int)rs);
     nkeys = __builtin_amdgcn_readfirstlane(nkeys);
-    if (nkeys <= 0) continue;
-    const int ntiles = (nkeys + KT - 1) / KT;
+    // an item without keys runs one fully masked tile: its output is 0 and
+    // its LSE -inf, and its step publishes the next item's slots like any other
+    nkeys = max(nkeys, 0);
+    const int ntiles = max(1, (nkeys + KT - 1) / KT);
     const uint32_t rs_bytes = (uint32_t)(rs * 2);
     const uint32_t kvoff = (uint32_t)r0 * rs_bytes;
 
@@ -229,32 +286,32 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       }
     };
 
-    // Q^T (B of S^T): lane holds row R = wave*32 + l32 -> (slot i, head j),
-    // dims 16 s + 8 g .. +8
+    // Q^T (B of S^T): lane holds row R -> (slot row_i, head row_j), dims
+    // 16 s + 8 g .. +8.  Rows past the item's queries take query slot 0's
+    // values: they are computed like any row and never stored, and the loads
+    // stay in flight until the first tile is in.
     u32x4_t qr[KS];
-    int qidx_r, qlim;
+    const int qidx_r = qidx_cur;
+    const int qlim = local ? (int)(a.chunk_start + qidx_cur - a.wstart) : 0x7fffffff;
     {
-      const int R = wave * 32 + l32;
-      const int i = R / G, j = R % G;
-      const bool ok = i < qn;
-      int qidx = 0;
-      if (ok) qidx = local ? qb + i : a.qvals[entry0 + i];
-      qidx_r = ok ? qidx : -1;
-      qlim = local ? (int)(a.chunk_start + qidx - a.wstart) : 0x7fffffff;
-      const bf16_t* src = a.q + (int64_t)qidx * a.q_sq + (int64_t)(h * G + j) * a.q_sh + g * 8;
+      const bf16_t* src = a.q + (int64_t)max(qidx_cur, 0) * a.q_sq + (int64_t)(h * G + row_j) * a.q_sh + g * 8;
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 16) : u32x4_t{0, 0, 0, 0};
+      for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 16);
     }
-    // the last key any row of this wave may see, and the last key every row sees
-    int wave_lim = qlim, wave_min = qidx_r >= 0 ? qlim : 0x7fffffff;
+    // the last key any row of this wave may see, and the last key every row
+    // sees (no limit inside a cluster item)
+    int wave_lim = 0x7fffffff, wave_min = 0x7fffffff;
+    if (local) {
+      wave_lim = qlim;
+      wave_min = qidx_r >= 0 ? qlim : 0x7fffffff;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
-      wave_min = min(wave_min, __shfl_xor(wave_min, o, 64));
+      for (int o = 1; o < 64; o <<= 1) {
+        wave_lim = max(wave_lim, __shfl_xor(wave_lim, o, 64));
+        wave_min = min(wave_min, __shfl_xor(wave_min, o, 64));
+      }
+      wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
+      wave_min = __builtin_amdgcn_readfirstlane(wave_min);
     }
-    wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
-    wave_min = __builtin_amdgcn_readfirstlane(wave_min);
 
     // S^T = K Q^T for one tile; K fragments are read KA_AHEAD ahead
     constexpr int KA_AHEAD = 3;
@@ -445,6 +502,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       lmax_all = NEG_INF;
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+      prefetch_queries();
       f32x16_t sA, sB;
       gemm_s(sA, kbuf_at(0));
       mask_track(sA, 0);
@@ -506,18 +564,27 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           const int c = (4 * dt + q4) ^ (l32 & (S::CH - 1));
           *reinterpret_cast<u32x2_t*>(stage + l32 * S::ROW_BYTES + 16 * c + 8 * g) = w;
         }
-      // read back whole rows: instruction m covers rows ROWS_PER_INST m ..
+      // read back whole rows (instruction m covers rows ROWS_PER_INST m ..),
+      // all reads first, then the stores, so no store waits on a single read
+      constexpr int NR = 32 / S::ROWS_PER_INST;
+      const int c16 = lane % S::CH;
 #pragma unroll
-      for (int m = 0; m < 32 / S::ROWS_PER_INST; ++m) {
-        const int r = m * S::ROWS_PER_INST + lane / S::CH;
-        const int c = lane % S::CH;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage + r * S::ROW_BYTES + 16 * (c ^ (r & (S::CH - 1))));
-        const int RR = wave * 32 + r;
-        const int i = RR / G, j = RR % G;
-        if (i < qn) {
+      for (int half = 0; half < 2; ++half) {
+        u32x4_t rows[NR / 2];
+#pragma unroll
+        for (int mm = 0; mm < NR / 2; ++mm) {
+          const int m = half * (NR / 2) + mm;
+          const int r = m * S::ROWS_PER_INST + lane / S::CH;
+          rows[mm] = *reinterpret_cast<const u32x4_t*>(stage + r * S::ROW_BYTES + 16 * (c16 ^ (r & (S::CH - 1))));
+        }
+#pragma unroll
+        for (int mm = 0; mm < NR / 2; ++mm) {
+          const int m = half * (NR / 2) + mm;
+          const int RR = wave * 32 + m * S::ROWS_PER_INST + lane / S::CH;
+          const int i = RR / G, j = RR % G;
           bf16_t* dst = local ? a.local_o + (int64_t)(qb + i) * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh
                               : a.part_o + ((entry0 + i) * G + j) * D;
-          *reinterpret_cast<u32x4_t*>(dst + 8 * c) = v;
+          if (i < qn) *reinterpret_cast<u32x4_t*>(dst + 8 * c16) = rows[mm];
         }
       }
     }
@@ -749,7 +816,7 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   a.nvis = nvis;
   a.rev_indptr = rev_indptr;
   a.qvals = qvals;
-  a.items = (const int4*)items;
+  a.items = (const PrefillItem*)items;
   a.queue = queue;
   a.part_o = (bf16_t*)part_o;
   a.part_lse = part_lse;

@@ -165,6 +165,17 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
   return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
+// One prefill work item, 32 bytes: written by the work-list builder and read
+// by the attention kernel.  For a cluster item (c >= 0) the builder resolves
+// everything the attention needs from the reverse index, so an item costs the
+// kernel one load: nkeys = visible rows of the cluster, entry0 = first partial
+// slot of the item (rev_indptr + qb), row0 = first packed row of the run.  A
+// local item (c < 0) leaves the last three at 0.
+struct __attribute__((aligned(32))) PrefillItem {
+  int h, c, qb, qn;
+  int nkeys, entry0, row0, pad;
+};
+
 #define SBSA_CHECK_LAUNCH()                                 \
   do {                                                      \
     if (hipGetLastError() != hipSuccess) return SBSA_ERR_LAUNCH; \

@@ -340,7 +340,10 @@ __device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, int
 
 __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __restrict__ rev_counts,
                                                            int hkv, int C, int Qc, int QT,
-                                                           int has_local, int4* __restrict__ items,
+                                                           int has_local, const int32_t* __restrict__ indptr,
+                                                           const int32_t* __restrict__ nvis,
+                                                           const int32_t* __restrict__ rev_indptr,
+                                                           PrefillItem* __restrict__ items,
                                                            int32_t* __restrict__ queue,
                                                            int64_t cap) {
   extern __shared__ int s_first[];     // [nsrc] first item of each source
@@ -397,7 +400,13 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
       if (pos >= cap) break;
       const int qb = si.c >= 0 ? j * QT : si.qb;
       const int qn = si.c >= 0 ? min(QT, si.qn - qb) : si.qn;
-      items[pos] = make_int4(si.h, si.c, qb, qn);
+      PrefillItem it{si.h, si.c, qb, qn, 0, 0, 0, 0};
+      if (si.c >= 0) {
+        it.nkeys = nvis[si.h * C + si.c];
+        it.entry0 = rev_indptr[si.h * C + si.c] + qb;
+        it.row0 = indptr[si.h * (C + 1) + si.c];
+      }
+      items[pos] = it;
     }
   }
   if (threadIdx.x < 8) {
@@ -523,9 +532,11 @@ int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
 }
 
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
-                       int num_queries, int queries_per_item, int has_local, void* items,
-                       int64_t items_cap, int32_t* queue, hipStream_t stream) {
+                       int num_queries, int queries_per_item, int has_local,
+                       const int32_t* indptr, const int32_t* nvis, const int32_t* rev_indptr,
+                       void* items, int64_t items_cap, int32_t* queue, hipStream_t stream) {
   if (!rev_counts || !items || !queue || queries_per_item < 1) return SBSA_ERR_ARG;
+  if (!indptr || !nvis || !rev_indptr) return SBSA_ERR_ARG;
   const int nloc = has_local ? (num_queries + queries_per_item - 1) / queries_per_item : 0;
   const size_t lds = (size_t)(nloc * num_kv_heads + num_kv_heads * num_clusters) * 4;
   if (lds > 96 * 1024) return SBSA_ERR_UNSUPPORTED;
@@ -537,7 +548,8 @@ int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clus
     configured = lds;
   }
   hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), lds, stream, rev_counts, num_kv_heads,
-                     num_clusters, num_queries, queries_per_item, has_local, (int4*)items, queue,
+                     num_clusters, num_queries, queries_per_item, has_local, indptr, nvis, rev_indptr,
+                     (PrefillItem*)items, queue,
                      items_cap);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;

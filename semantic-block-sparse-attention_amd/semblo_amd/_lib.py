@@ -36,7 +36,7 @@ SIGNATURES = {
     "sbsa_causal_sizes": (I32, [P, I64, P, P, I32, I32, I64, P, P]),
     "sbsa_reverse_index": (I32, [P, I32, I32, I32, P, P, P, P, P, I64, P, P]),
     "sbsa_prefill_items_bound": (I64, [I64, I32, I32, I32, I32]),
-    "sbsa_prefill_items": (I32, [P, I32, I32, I32, I32, I32, P, I64, P, P]),
+    "sbsa_prefill_items": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, I64, P, P]),
     "sbsa_prefill_item_rows": (I32, []),
     "sbsa_prefill_attend": (I32, [P, I64, I64, I32, I32, I32, I32, P, I64, P, P, I64, I64, P, P,
                                   I32, P, P, P, P, P, P, P, I64, I64, P, I64, I64, F32, I32, P]),

@@ -22,6 +22,11 @@ import torch
 
 from . import _lib
 
+# int32 fields of one work item {head, cluster, first query slot, count,
+# visible rows, first partial slot, first packed row, 0}
+ITEM_INTS = 8
+
+
 def queries_per_item(q_per_kv: int) -> int:
     """Queries of one work item: the kernel's (query, head) rows per item over G."""
     return _lib.query("sbsa_prefill_item_rows") // q_per_kv
@@ -130,11 +135,11 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     local_lse = torch.empty(qn, hq, dtype=torch.float32, device=dev)
     qt = queries_per_item(g)
     bound = _lib.query("sbsa_prefill_items_bound", nnz, qn, hkv, c, qt)
-    items = torch.empty(max(bound, 1), 4, dtype=torch.int32, device=dev)
+    items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
     queue = torch.empty(24, dtype=torch.int32, device=dev)
     s = _lib.stream(dev)
-    _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(items), bound,
-              _lib.ptr(queue), s)
+    _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
+              _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
@@ -174,13 +179,14 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     qt = queries_per_item(g)
     zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
     bound = hkv * ((qn + qt - 1) // qt) + 1
-    items = torch.empty(bound, 4, dtype=torch.int32, device=dev)
+    items = torch.empty(bound, ITEM_INTS, dtype=torch.int32, device=dev)
     queue = torch.empty(24, dtype=torch.int32, device=dev)
     if out is None:
         out = torch.empty_like(q)
     s = _lib.stream(dev)
-    _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(items),
-              bound, _lib.ptr(queue), s)
+    # no cluster has queries: the index arrays are never read
+    _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(zero_counts),
+              _lib.ptr(zero_counts), _lib.ptr(zero_counts), _lib.ptr(items), bound, _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s)
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,

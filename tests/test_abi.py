@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
     for name, n in decls.items():
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
         assert len(_lib.SIGNATURES[name][1]) == n, f"{name}: header {n} args, binding {len(_lib.SIGNATURES[name][1])}"
-    assert lib.sbsa_abi_version() == 2
+    assert lib.sbsa_abi_version() == 3
 
 
 def test_size_queries_run_without_a_gpu():
