@@ -102,7 +102,12 @@ struct AttnTileShape {
   static constexpr int CH = D / 8;                    // 16-byte chunks per row
   static constexpr int ROW_BYTES = D * 2;
   static constexpr int TILE_BYTES = KT * ROW_BYTES;   // one of K or V
-  static constexpr size_t LDS_BYTES = 4 * (size_t)TILE_BYTES;   // K, K, V, V
+  // K, K, V, V tiles; the pipelined kernel adds a staging area for its
+  // epilogue (one 32-row slice per wave), the other stages in the tile buffers
+  static constexpr size_t stage_offset(bool pipe) { return pipe ? 4 * (size_t)TILE_BYTES : 0; }
+  static constexpr size_t lds_bytes(bool pipe) {
+    return 4 * (size_t)TILE_BYTES + (pipe ? (size_t)PREFILL_ROWS * ROW_BYTES : 0);
+  }
   static constexpr int ROWS_PER_INST = 64 / CH;       // rows one wave instruction covers
   static constexpr int INSTS = KT / ROWS_PER_INST;    // instructions per K (or V) tile
   static constexpr int PER_WAVE = INSTS / 4;
@@ -114,7 +119,12 @@ struct AttnTileShape {
 // 8 (i / 4) + 4 (l / 32) + i % 4, i < 16, which are exactly the B operand
 // P^T of the two 16-key steps of O^T (keys {0-3, 8-11 | 4-7, 12-15} and
 // {16-19, 24-27 | 20-23, 28-31}), so the probabilities never leave the lane.
-template <int D, int G>
+// PIPE: the next item's Q and first tiles are loaded while this item's
+// epilogue runs, which needs a staging area of its own (128 KB of LDS in all
+// at D = 256).  The kernel of the dense chunks, which run beside the index
+// build, stays at 64 KB of LDS and under 384 registers per lane so that the
+// build's kernels fit on the same compute units.
+template <int D, int G, bool PIPE>
 __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   using S = AttnTileShape<D>;
   constexpr int KS = D / 16;        // 16-dim steps of S^T
@@ -212,6 +222,80 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
 #pragma unroll
     for (int k = 0; k < PREFILL_ROWS / G; k += 64) lds_dma4(rsrc, dst + 4 * k, (uint32_t)(lane + k) * 4u);
   };
+  // direct loads of the K (or V) rows of tile t into an LDS buffer; rows
+  // past the item's last key are outside the buffer range and read as 0
+  auto issue = [&](const bf16_t* base, uint32_t rs_bytes, int nkeys, int t, unsigned char* dst_tile, bool is_k) {
+    const int t0 = t * KT;
+    const int valid = __builtin_amdgcn_readfirstlane((int)((uint32_t)(nkeys - t0) * rs_bytes));
+    const uint64_t b = (uint64_t)((const unsigned char*)base + (uint64_t)t0 * rs_bytes);
+    u32x4_t rsrc;     // raw buffer resource: base, stride 0, valid bytes, config
+    rsrc.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    rsrc.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
+    rsrc.z = (uint32_t)valid;
+    rsrc.w = (uint32_t)BUFFER_CONFIG;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(lds_void_t*)(dst_tile + wave * 1024));
+    const uint32_t kvoff = (uint32_t)r0 * rs_bytes;
+#pragma unroll
+    for (int m = 0; m < S::PER_WAVE; ++m) {
+      const uint32_t roff = kvoff + (uint32_t)(m * 4 * S::ROWS_PER_INST) * rs_bytes;
+      const uint32_t slot = is_k ? kslot[m & 1] : vslot;
+      lds_dma16(rsrc, dst + m * 4096, roff + slot);
+    }
+  };
+
+  // The item being started: its fields (uniform), this lane's query (-1 past
+  // the item's queries; a cluster item's slots were loaded into LDS during the
+  // previous item), its Q rows in registers and its first tiles in flight.
+  // An item is started as soon as the previous one no longer needs its Q
+  // registers and tile buffers, so these loads run under that item's
+  // epilogue.  Q^T (B of S^T): lane holds row R -> (slot row_i, head row_j),
+  // dims 16 s + 8 g .. +8.  Rows past the item's queries take query slot 0's
+  // values: they are computed like any row and never stored.
+  int b_h = 0, b_c = 0, b_qb = 0, b_qn = 0, b_nkeys = 0, b_qidx = -1;
+  int64_t b_entry0 = 0;
+  const bf16_t* b_kp = nullptr;
+  const bf16_t* b_vp = nullptr;
+  uint32_t b_rsb = 0;
+  u32x4_t qr[KS];
+  auto begin = [&](const PrefillItem& r) {
+    b_h = __builtin_amdgcn_readfirstlane(r.h);
+    b_c = __builtin_amdgcn_readfirstlane(r.c);
+    b_qb = __builtin_amdgcn_readfirstlane(r.qb);
+    b_qn = __builtin_amdgcn_readfirstlane(r.qn);
+    b_entry0 = __builtin_amdgcn_readfirstlane(r.entry0);
+    const bool local = b_c < 0;
+    const int64_t row0 = __builtin_amdgcn_readfirstlane(r.row0);
+    int nkeys = local ? (int)(a.chunk_start + b_qb + b_qn - a.wstart) : __builtin_amdgcn_readfirstlane(r.nkeys);
+    // an item without keys runs one fully masked tile: its output is 0 and its
+    // LSE -inf, and its step publishes the next item's slots like any other
+    b_nkeys = max(__builtin_amdgcn_readfirstlane(nkeys), 0);
+    const bf16_t* kp;
+    const bf16_t* vp;
+    int64_t rs;
+    if (local) {
+      kp = a.korig + (int64_t)b_h * a.o_sh;   // row 0 is position wstart
+      vp = a.vorig + (int64_t)b_h * a.o_sh;
+      rs = a.o_st;
+    } else {
+      kp = a.packed + row0 * a.Hkv * D + (int64_t)b_h * D;
+      vp = kp + a.packed_len * a.Hkv * D;
+      rs = (int64_t)a.Hkv * D;
+    }
+    // uniform values (scalar registers): the buffer resources built from them
+    // need no per-lane loop
+    b_kp = uniform_ptr(kp);
+    b_vp = uniform_ptr(vp);
+    b_rsb = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rs * 2));
+    b_qidx = row_i >= b_qn ? -1 : (local ? b_qb + row_i : s_qslots[row_i]);
+    const bf16_t* src = a.q + (int64_t)max(b_qidx, 0) * a.q_sq + (int64_t)(b_h * G + row_j) * a.q_sh + g * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 16);
+    issue(b_kp, b_rsb, b_nkeys, 0, kbuf_at(0), true);
+    issue(b_vp, b_rsb, b_nkeys, 0, vbuf_at(0), false);
+    if (b_nkeys > KT) issue(b_kp, b_rsb, b_nkeys, 1, kbuf_at(1), true);
+  };
+
   PrefillItem rec{};
   int idx = next_index();
   if (idx >= 0) {
@@ -219,85 +303,31 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     fetch_slots(rec);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    begin(rec);
   }
   int idx_n = -1;
   for (; idx >= 0; idx = idx_n) {
-    const int h = __builtin_amdgcn_readfirstlane(rec.h), c = __builtin_amdgcn_readfirstlane(rec.c);
-    const int qb = __builtin_amdgcn_readfirstlane(rec.qb), qn = __builtin_amdgcn_readfirstlane(rec.qn);
-    const int64_t entry0 = __builtin_amdgcn_readfirstlane(rec.entry0);
-    const int64_t row0 = __builtin_amdgcn_readfirstlane(rec.row0);
+    // this item, as begin() left it
+    const int h = __builtin_amdgcn_readfirstlane(b_h), c = __builtin_amdgcn_readfirstlane(b_c);
+    const int qb = __builtin_amdgcn_readfirstlane(b_qb), qn = __builtin_amdgcn_readfirstlane(b_qn);
+    const int64_t entry0 = b_entry0;
+    const int nkeys = __builtin_amdgcn_readfirstlane(b_nkeys);
+    const bf16_t* const kp = b_kp;
+    const bf16_t* const vp = b_vp;
+    const uint32_t rs_bytes = b_rsb;
+    const int qidx_r = b_qidx;
     const bool local = c < 0;
-    // this lane's query (-1 past the item's queries); a cluster item's slots
-    // were loaded into LDS during the previous item
-    const int qidx_cur = row_i >= qn ? -1 : (local ? qb + row_i : s_qslots[row_i]);
-    int nkeys = local ? (int)(a.chunk_start + qb + qn - a.wstart) : __builtin_amdgcn_readfirstlane(rec.nkeys);
+    const int ntiles = max(1, (nkeys + KT - 1) / KT);
     idx_n = next_index();
     if (idx_n >= 0) rec = a.items[idx_n];
     // once, after this item's first tiles are in (every wave has read its
-    // slot by then); the next item's first step, or its own wait, publishes it
+    // slot by then); the next item's first step publishes it
     bool prefetched = false;
     auto prefetch_queries = [&]() {
       if (idx_n >= 0 && !prefetched) fetch_slots(rec);
       prefetched = true;
     };
-    const bf16_t* kp;
-    const bf16_t* vp;
-    int64_t rs;
-    if (local) {
-      kp = a.korig + (int64_t)h * a.o_sh;   // row 0 is position wstart
-      vp = a.vorig + (int64_t)h * a.o_sh;
-      rs = a.o_st;
-    } else {
-      kp = a.packed + row0 * a.Hkv * D + (int64_t)h * D;
-      vp = kp + a.packed_len * a.Hkv * D;
-      rs = (int64_t)a.Hkv * D;
-    }
-    // uniform values (scalar registers): the buffer resources built from them
-    // need no per-lane loop
-    kp = uniform_ptr(kp);
-    vp = uniform_ptr(vp);
-    rs = __builtin_amdgcn_readfirstlane((int)rs);
-    nkeys = __builtin_amdgcn_readfirstlane(nkeys);
-    // an item without keys runs one fully masked tile: its output is 0 and
-    // its LSE -inf, and its step publishes the next item's slots like any other
-    nkeys = max(nkeys, 0);
-    const int ntiles = max(1, (nkeys + KT - 1) / KT);
-    const uint32_t rs_bytes = (uint32_t)(rs * 2);
-    const uint32_t kvoff = (uint32_t)r0 * rs_bytes;
-
-    // direct loads of the K (or V) rows of tile t into an LDS buffer; rows
-    // past the item's last key are outside the buffer range and read as 0
-    auto issue = [&](const bf16_t* base, int t, unsigned char* dst_tile, bool is_k) {
-      const int t0 = t * KT;
-      const int valid = __builtin_amdgcn_readfirstlane((int)((uint32_t)(nkeys - t0) * rs_bytes));
-      const uint64_t b = (uint64_t)(base + (int64_t)t0 * rs);
-      u32x4_t rsrc;     // raw buffer resource: base, stride 0, valid bytes, config
-      rsrc.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
-      rsrc.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
-      rsrc.z = (uint32_t)valid;
-      rsrc.w = (uint32_t)BUFFER_CONFIG;
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          (uint32_t)(uintptr_t)(lds_void_t*)(dst_tile + wave * 1024));
-#pragma unroll
-      for (int m = 0; m < S::PER_WAVE; ++m) {
-        const uint32_t roff = kvoff + (uint32_t)(m * 4 * S::ROWS_PER_INST) * rs_bytes;
-        const uint32_t slot = is_k ? kslot[m & 1] : vslot;
-        lds_dma16(rsrc, dst + m * 4096, roff + slot);
-      }
-    };
-
-    // Q^T (B of S^T): lane holds row R -> (slot row_i, head row_j), dims
-    // 16 s + 8 g .. +8.  Rows past the item's queries take query slot 0's
-    // values: they are computed like any row and never stored, and the loads
-    // stay in flight until the first tile is in.
-    u32x4_t qr[KS];
-    const int qidx_r = qidx_cur;
-    const int qlim = local ? (int)(a.chunk_start + qidx_cur - a.wstart) : 0x7fffffff;
-    {
-      const bf16_t* src = a.q + (int64_t)max(qidx_cur, 0) * a.q_sq + (int64_t)(h * G + row_j) * a.q_sh + g * 8;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 16);
-    }
+    const int qlim = local ? (int)(a.chunk_start + qidx_r - a.wstart) : 0x7fffffff;
     // the last key any row of this wave may see, and the last key every row
     // sees (no limit inside a cluster item)
     int wave_lim = 0x7fffffff, wave_min = 0x7fffffff;
@@ -435,8 +465,8 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     // last active tile and the tiles past every row of the wave, whose loads
     // the wave still issues for the others.
     auto issue_next = [&](int t) {
-      if (t + 2 < ntiles) issue(kp, t + 2, kbuf_at(t & 1), true);
-      if (t + 1 < ntiles) issue(vp, t + 1, vbuf_at((t + 1) & 1), false);
+      if (t + 2 < ntiles) issue(kp, rs_bytes, nkeys, t + 2, kbuf_at(t & 1), true);
+      if (t + 1 < ntiles) issue(vp, rs_bytes, nkeys, t + 1, vbuf_at((t + 1) & 1), false);
     };
     auto finish_step = [&]() {
       __builtin_amdgcn_s_waitcnt(0);
@@ -491,9 +521,11 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     // maxima, and the last pass takes them as reference.
     for (int pass = 0; pass < 3; ++pass) {
       const bool sweep = pass == 1;
-      issue(kp, 0, kbuf_at(0), true);
-      issue(vp, 0, vbuf_at(0), false);
-      if (ntiles > 1) issue(kp, 1, kbuf_at(1), true);
+      if (pass > 0) {           // pass 0's first tiles were issued by begin()
+        issue(kp, rs_bytes, nkeys, 0, kbuf_at(0), true);
+        issue(vp, rs_bytes, nkeys, 0, vbuf_at(0), false);
+        if (ntiles > 1) issue(kp, rs_bytes, nkeys, 1, kbuf_at(1), true);
+      }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -536,24 +568,26 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       }
     }
 
+    // PIPE: the next item's Q and first tiles load under this item's epilogue
+    if (PIPE && idx_n >= 0) begin(rec);
+
     // epilogue: normalise, then write the partial (or the local window) and
-    // its LSE.  The rows go through this wave's own 32-row slice of the (now
-    // idle) tile buffers, so that every store is 16 bytes per lane and whole
-    // rows per instruction: the item's rows are contiguous in part_o, and
-    // the G heads of a query are contiguous in the window output.
+    // its LSE.  The rows go through this wave's own 32-row slice of a staging
+    // area (PIPE: its own; otherwise the idle tile buffers), so that every
+    // store is 16 bytes per lane and whole rows per instruction: the item's
+    // rows are contiguous in part_o, and the G heads of a query are
+    // contiguous in the window output.
     {
       const float l = l_part + __shfl_xor(l_part, 32, 64);
-      const int R = wave * 32 + l32;
       const float inv = (l > 0.f) ? 1.0f / l : 0.f;
       if (qidx_r >= 0 && g == 0) {
-        const int i = R / G, j = R % G;
         const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
-        float* ldst = local ? (a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + j : nullptr)
-                            : a.part_lse + (entry0 + i) * G + j;
+        float* ldst = local ? (a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + row_j : nullptr)
+                            : a.part_lse + (entry0 + row_i) * G + row_j;
         if (ldst) *ldst = lse;
       }
       // 16-byte chunk c of row r sits at chunk c ^ (r % 32) of the row
-      unsigned char* stage = smem_attn + wave * 32 * S::ROW_BYTES;
+      unsigned char* stage = smem_attn + S::stage_offset(PIPE) + wave * 32 * S::ROW_BYTES;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -565,7 +599,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           *reinterpret_cast<u32x2_t*>(stage + l32 * S::ROW_BYTES + 16 * c + 8 * g) = w;
         }
       // read back whole rows (instruction m covers rows ROWS_PER_INST m ..),
-      // all reads first, then the stores, so no store waits on a single read
+      // reads first, then the stores, so no store waits on a single read
       constexpr int NR = 32 / S::ROWS_PER_INST;
       const int c16 = lane % S::CH;
 #pragma unroll
@@ -587,6 +621,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           if (i < qn) *reinterpret_cast<u32x4_t*>(dst + 8 * c16) = rows[mm];
         }
       }
+    }
+    if (!PIPE && idx_n >= 0) {
+      __syncthreads();          // every wave is done with its staging rows
+      begin(rec);
     }
   }
 }
@@ -719,29 +757,38 @@ __global__ __launch_bounds__(256) void combine_kernel(
   if (out_lse && (lane * E) % D == 0) out_lse[(int64_t)qi * Hq + h * G + j] = mx + logf(den);
 }
 
-template <int D, int G>
-int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
-  const size_t lds = AttnTileShape<D>::LDS_BYTES;
+template <int D, int G, bool PIPE>
+int launch_attn_kernel(const AttnArgs& a, int grid, hipStream_t stream) {
+  const size_t lds = AttnTileShape<D>::lds_bytes(PIPE);
   static bool configured = false;
   if (!configured) {
-    hipFuncSetAttribute((const void*)attn_items_kernel<D, G>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (hipFuncSetAttribute((const void*)attn_items_kernel<D, G, PIPE>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return SBSA_ERR_UNSUPPORTED;
     configured = true;
   }
   static int auto_grid = 0;
   if (grid <= 0) {
     if (!auto_grid) {
       int dev = 0, cus = 0, occ = 0;
-      hipGetDevice(&dev);
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)attn_items_kernel<D, G>,
-                                                   256, lds);
+      (void)hipGetDevice(&dev);
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)attn_items_kernel<D, G, PIPE>,
+                                                         256, lds);
       auto_grid = (cus > 0 ? cus : 256) * (occ > 0 ? occ : 1);
     }
     grid = auto_grid;
   }
-  hipLaunchKernelGGL((attn_items_kernel<D, G>), dim3(grid), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL((attn_items_kernel<D, G, PIPE>), dim3(grid), dim3(256), lds, stream, a);
   return SBSA_OK;
+}
+
+// the pipelined kernel for chunks with cluster items (sparse chunks, which
+// run after the index build), the compact one for dense chunks
+template <int D, int G>
+int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
+  return a.packed ? launch_attn_kernel<D, G, true>(a, grid, stream)
+                  : launch_attn_kernel<D, G, false>(a, grid, stream);
 }
 
 template <int D, int G>
