@@ -23,6 +23,7 @@ namespace {
 struct AttnArgs {
   const bf16_t* q;          // [Qc, Hq, D] chunk queries
   int64_t q_sq, q_sh;
+  int64_t q_bytes;          // extent of q in bytes (buffer range of the staged Q loads)
   const bf16_t* packed;     // [2, Lp, Hkv, D] cluster-ordered K/V
   int64_t packed_len;
   const bf16_t* korig;      // prompt-order keys from position wstart: k[pos - wstart, h, :]
@@ -258,6 +259,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   const bf16_t* b_vp = nullptr;
   uint32_t b_rsb = 0;
   u32x4_t qr[KS];
+  bool q_staged = false;      // PIPE: the next item's Q rows are in the staging area
   auto begin = [&](const PrefillItem& r) {
     b_h = __builtin_amdgcn_readfirstlane(r.h);
     b_c = __builtin_amdgcn_readfirstlane(r.c);
@@ -288,9 +290,20 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     b_vp = uniform_ptr(vp);
     b_rsb = (uint32_t)__builtin_amdgcn_readfirstlane((int)(rs * 2));
     b_qidx = row_i >= b_qn ? -1 : (local ? b_qb + row_i : s_qslots[row_i]);
-    const bf16_t* src = a.q + (int64_t)max(b_qidx, 0) * a.q_sq + (int64_t)(b_h * G + row_j) * a.q_sh + g * 8;
+    if (PIPE && q_staged) {
+      // the wave's rows were loaded into its staging slice during the
+      // previous item (K-tile layout): wait for its own loads, then read
+      __builtin_amdgcn_s_waitcnt(0);
+      const unsigned char* sq = smem_attn + S::stage_offset(true) + wave * 32 * S::ROW_BYTES;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 16);
+      for (int s = 0; s < KS; ++s)
+        qr[s] = *reinterpret_cast<const u32x4_t*>(sq + kbase[s & 7] + 256 * (s >> 3));
+    } else {
+      const bf16_t* src = a.q + (int64_t)max(b_qidx, 0) * a.q_sq + (int64_t)(b_h * G + row_j) * a.q_sh + g * 8;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 16);
+    }
+    q_staged = false;
     issue(b_kp, b_rsb, b_nkeys, 0, kbuf_at(0), true);
     issue(b_vp, b_rsb, b_nkeys, 0, vbuf_at(0), false);
     if (b_nkeys > KT) issue(b_kp, b_rsb, b_nkeys, 1, kbuf_at(1), true);
@@ -464,16 +477,56 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     // code the scheduler can interleave; the general one handles the wave's
     // last active tile and the tiles past every row of the wave, whose loads
     // the wave still issues for the others.
-    auto issue_next = [&](int t) {
+    // PIPE: the next item's Q rows into this wave's staging slice, in the
+    // K-tile layout (row r, 16-byte chunk c at slot (c % 16 ^ r % 16) + 16 (c / 16));
+    // issued in step 1, once the next item's query slots are published, after
+    // that step's tile loads, so the step's wait can leave them in flight
+    constexpr int QN = 32 / S::ROWS_PER_INST;      // loads per wave
+    auto stage_q = [&]() {
+      const int nh = __builtin_amdgcn_readfirstlane(rec.h), nc = __builtin_amdgcn_readfirstlane(rec.c);
+      const int nqb = __builtin_amdgcn_readfirstlane(rec.qb), nqn = __builtin_amdgcn_readfirstlane(rec.qn);
+      const uint64_t b = (uint64_t)a.q;
+      u32x4_t rsrc;
+      rsrc.x = __builtin_amdgcn_readfirstlane((uint32_t)b);
+      rsrc.y = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) & 0xffffu;
+      rsrc.z = (uint32_t)a.q_bytes;
+      rsrc.w = (uint32_t)BUFFER_CONFIG;
+      const uint32_t dst = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)(
+          smem_attn + S::stage_offset(true) + wave * 32 * S::ROW_BYTES));
+      const int p = lane % S::CH;
+#pragma unroll
+      for (int m = 0; m < QN; ++m) {
+        const int r = m * S::ROWS_PER_INST + lane / S::CH;
+        const int R = wave * 32 + r, i = R / G, j = R % G;
+        const int qi = i < nqn ? (nc < 0 ? nqb + i : s_qslots[i]) : -1;
+        const int cg = ((p & 15) ^ (r & 15)) + 16 * (p >> 4);
+        const uint32_t off = qi < 0 ? 0x80000000u
+                                    : (uint32_t)(((int64_t)qi * a.q_sq + (int64_t)(nh * G + j) * a.q_sh) * 2 + 16 * cg);
+        lds_dma16(rsrc, dst + m * S::ROWS_PER_INST * S::ROW_BYTES, off);
+      }
+    };
+    // returns whether this step staged the next item's Q
+    auto issue_next = [&](int t) -> bool {
       if (t + 2 < ntiles) issue(kp, rs_bytes, nkeys, t + 2, kbuf_at(t & 1), true);
       if (t + 1 < ntiles) issue(vp, rs_bytes, nkeys, t + 1, vbuf_at((t + 1) & 1), false);
+      if (PIPE && t == 1 && idx_n >= 0 && !q_staged) {
+        stage_q();
+        q_staged = true;
+        return true;
+      }
+      return false;
     };
-    auto finish_step = [&]() {
-      __builtin_amdgcn_s_waitcnt(0);
+    auto finish_step = [&](bool staged) {
+      if (staged) {
+        // every load but this step's QN staging loads (vmcnt QN, lgkmcnt 0)
+        __builtin_amdgcn_s_waitcnt((QN & 15) | ((QN >> 4) << 14) | (7 << 4));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
       __syncthreads();
     };
     auto step_full = [&](int t, f32x16_t& cur, f32x16_t& nxt) {
-      issue_next(t);
+      const bool staged = issue_next(t);
       mask_only(cur, t);
       u32x4_t pb[2];
       gemm_s_body(nxt, kbuf_at((t + 1) & 1));
@@ -492,12 +545,12 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       }
       gemm_pv(pb, vbuf_at(t & 1));
-      finish_step();
+      finish_step(staged);
     };
     // the general form, for the tiles around a wave's last active one; with
     // sweep set it only tracks the rows' maxima (no probabilities, no O)
     auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt, bool sweep) {
-      issue_next(t);
+      const bool staged = issue_next(t);
       const bool act = t * KT <= wave_lim;
       const bool act_n = t + 1 < ntiles && (t + 1) * KT <= wave_lim;
       u32x4_t pb[2];
@@ -510,7 +563,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         exp_pack(cur, pb);
         gemm_pv(pb, vbuf_at(t & 1));
       }
-      finish_step();
+      finish_step(staged);
     };
 
     // Each row's probabilities are taken against a reference maximum fixed
@@ -784,11 +837,12 @@ int launch_attn_kernel(const AttnArgs& a, int grid, hipStream_t stream) {
 }
 
 // the pipelined kernel for chunks with cluster items (sparse chunks, which
-// run after the index build), the compact one for dense chunks
+// run after the index build), the compact one for dense chunks; the
+// pipelined kernel's staged Q loads address q with 31-bit offsets
 template <int D, int G>
 int launch_attn(const AttnArgs& a, int grid, hipStream_t stream) {
-  return a.packed ? launch_attn_kernel<D, G, true>(a, grid, stream)
-                  : launch_attn_kernel<D, G, false>(a, grid, stream);
+  return a.packed && a.q_bytes < 0x7fffffff ? launch_attn_kernel<D, G, true>(a, grid, stream)
+                                            : launch_attn_kernel<D, G, false>(a, grid, stream);
 }
 
 template <int D, int G>
@@ -853,6 +907,7 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   a.q = (const bf16_t*)q;
   a.q_sq = q_sq;
   a.q_sh = q_sh;
+  a.q_bytes = ((int64_t)(num_queries - 1) * q_sq + (int64_t)(num_q_heads - 1) * q_sh + dim) * 2;
   a.packed = (const bf16_t*)packed;
   a.packed_len = packed_len;
   a.korig = (const bf16_t*)k_orig;
