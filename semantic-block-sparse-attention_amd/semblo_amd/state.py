@@ -33,6 +33,31 @@ from .config import num_flat_clusters
 PACK_ALIGN = 256
 
 
+class _DrawBuffers:
+    """Host buffers of the build's random draws, kept across builds of the same
+    shape: the permutations are drawn into them (no fresh host pages per draw)
+    and the sample and initial rows go to the device from pinned memory."""
+
+    def __init__(self, length: int, fit_n: int, c: int):
+        self.perm = torch.empty(length, dtype=torch.int64)
+        self.sub = torch.empty(fit_n, dtype=torch.int64)
+        self.pinned = torch.empty(fit_n + c, dtype=torch.int32, pin_memory=True)
+        self.uploaded = None            # event after the last upload from `pinned`
+
+
+_DRAW_BUFFERS: dict = {}
+
+
+def _draw_buffers(length: int, fit_n: int, c: int) -> _DrawBuffers:
+    key = (length, fit_n, c)
+    buf = _DRAW_BUFFERS.get(key)
+    if buf is None:
+        if len(_DRAW_BUFFERS) >= 4:
+            _DRAW_BUFFERS.clear()
+        buf = _DRAW_BUFFERS[key] = _DrawBuffers(length, fit_n, c)
+    return buf
+
+
 @dataclass
 class ProductPostingIndex:
     """Flat-partition index of one layer's prompt (state.py:372-475 fields)."""
@@ -139,12 +164,21 @@ class ProductPostingIndex:
         ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
+        host = _draw_buffers(length, fit_n, c)
+
         def draw_sample_and_init():
             # fit_flat_codebook's first two draws (flat_index.py:237-262)
-            perm = torch.randperm(length, generator=gen)
-            sample = perm[:fit_n].to(torch.int32).to(dev)
-            init = torch.randperm(fit_n, generator=gen)[:c].to(torch.int32).to(dev)
-            return sample, init
+            torch.randperm(length, generator=gen, out=host.perm)
+            torch.randperm(fit_n, generator=gen, out=host.sub)
+            if host.uploaded is not None:
+                host.uploaded.synchronize()     # the previous upload has left `pinned`
+            host.pinned[:fit_n].copy_(host.perm[:fit_n])
+            host.pinned[fit_n:].copy_(host.sub[:c])
+            both = torch.empty(fit_n + c, dtype=torch.int32, device=dev)
+            both.copy_(host.pinned, non_blocking=True)
+            host.uploaded = torch.cuda.Event()
+            host.uploaded.record()
+            return both[:fit_n], both[fit_n:]
 
         def iterate(start, sample_idx):
             # k-means steps start.. with no restart rows; an iteration that left a
@@ -182,7 +216,8 @@ class ProductPostingIndex:
                 # (flat_index.py:277-283), then the later iterations again
                 empty = counts_host[it] == 0
                 src = torch.full((c,), -1, dtype=torch.int32)
-                src[empty] = torch.randperm(fit_n, generator=gen)[:int(empty.sum())].to(torch.int32)
+                torch.randperm(fit_n, generator=gen, out=host.sub)
+                src[empty] = host.sub[:int(empty.sum())].to(torch.int32)
                 src_d = src.to(dev)
                 _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
                           _lib.ptr(src_d), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
