@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=None)
@@ -195,6 +195,18 @@ def cpu_baseline(inp, layer, cfg, sample_queries):
             "build_ms": round(build_s * 1000.0, 1), "attention_ms": round(attn_s * 1000.0, 1)}
 
 
+def measured_traffic(config: int):
+    """HBM bytes per attention launch (mean over one prefill's launches) from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of this configuration, or None."""
+    path = ROOT / "profiles" / f"attn_items_kernel_config{config}_traffic.md"
+    if not path.exists():
+        return None
+    for text in path.read_text().splitlines():
+        if text.startswith("traffic_bytes_per_launch:"):
+            return float(text.split(":", 1)[1])
+    return None
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -316,7 +328,8 @@ def main():
         "roofline": None if "achieved" not in result else {
             "bound": "mfma", "achieved": round(result["achieved"], 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(result["achieved"] / PEAK_BF16_TFLOPS, 4),
-            "traffic": None, "kernel": "attn_items_kernel<256,4>",
+            "traffic": measured_traffic(args.config),
+            "kernel": "attn_items_kernel<256,4,*> (dense chunks: compact form, sparse chunks: pipelined form)",
             "flops_per_layer": result["flops"], "kernel_ms_per_layer": round(result["attn_ms"], 3),
             "launches_per_layer": result["launches"]},
         "decode_roofline": None if "decode_us" not in result else {
