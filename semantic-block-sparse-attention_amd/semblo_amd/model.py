@@ -155,30 +155,45 @@ class SembloAttention:
         side = self._build_stream(q.device)
         side.wait_event(inputs_ready)
         sparse = [(st, min(length, st + step)) for st in range(0, length, step) if st > cap]
+        # every sparse chunk's selection and reverse index on the build stream,
+        # each followed by a copy of its partial count to pinned host memory and
+        # an event; a chunk's attention starts as soon as its own plan is done,
+        # and the later plans run beside it
+        nnz_host = torch.empty(max(len(sparse), 1), dtype=torch.int64, pin_memory=True)
+        plans, ready = [], []
         with torch.cuda.stream(side):
             index = self._ingest_prompt_kv(kp, kk, vv)
             snapshot = CausalSnapshot(index)
-            # every sparse chunk's selection and reverse index, then one host read
-            # of all their partial counts (in place of one read per chunk)
-            plans = [fused_chunk_plan(q[st:en], self._query_state(qp[st:en]), index, snapshot, st,
+            for i, (st, en) in enumerate(sparse):
+                pl = fused_chunk_plan(q[st:en], self._query_state(qp[st:en]), index, snapshot, st,
                                       en - 1, temperature=cfg.selection_temperature,
                                       beta=cfg.bucket_size_penalty, target_tokens=self.target_tokens,
                                       iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x)
-                     for st, en in sparse]
-            nnz = torch.cat([pl.kv.nnz_d for pl in plans]).cpu().tolist() if plans else []
-            planned = torch.cuda.Event()
-            planned.record(side)
-        main.wait_event(planned)
-        for t in (index.codebooks, index.posting_positions, index.bucket_indptr, index.bucket_sizes,
-                  index._inverse_positions, index.packed_kv):
-            t.record_stream(main)
-        for pl in plans:
+                nnz_host[i:i + 1].copy_(pl.kv.nnz_d, non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record(side)
+                plans.append(pl)
+                ready.append(ev)
+            built = torch.cuda.Event()
+            built.record(side)
+        self.index = index
+        for i, ((st, en), pl) in enumerate(zip(sparse, plans)):
+            ready[i].synchronize()          # this chunk's partial count is on the host
+            main.wait_event(ready[i])
+            if i == 0:
+                for t in (index.codebooks, index.posting_positions, index.bucket_indptr,
+                          index.bucket_sizes, index._inverse_positions, index.packed_kv):
+                    t.record_stream(main)
             for t in pl.tensors():
                 t.record_stream(main)
-        self.index = index
-        for (st, en), pl, n in zip(sparse, plans, nnz):
-            fused_chunk_execute(pl, q[st:en], index, int(n),
+            fused_chunk_execute(pl, q[st:en], index, int(nnz_host[i]),
                                 sm_scale=self.scaling, out=out[st:en], timing=timing)
+        # the decode state uses the index on this stream
+        main.wait_event(built)
+        if not sparse:
+            for t in (index.codebooks, index.posting_positions, index.bucket_indptr,
+                      index.bucket_sizes, index._inverse_positions, index.packed_kv):
+                t.record_stream(main)
         self.adopt_index(index)
         return output
 
