@@ -157,14 +157,18 @@ class SembloAttention:
         sparse = [(st, min(length, st + step)) for st in range(0, length, step) if st > cap]
         # every sparse chunk's selection and reverse index on the build stream,
         # each followed by a copy of its partial count to pinned host memory and
-        # an event; a chunk's attention starts as soon as its own plan is done,
-        # and the later plans run beside it
+        # an event.  Plans are enqueued one chunk ahead of the attention: a
+        # chunk's attention starts as soon as its own plan is done, and the
+        # next plan runs beside it.
         nnz_host = torch.empty(max(len(sparse), 1), dtype=torch.int64, pin_memory=True)
         plans, ready = [], []
         with torch.cuda.stream(side):
             index = self._ingest_prompt_kv(kp, kk, vv)
             snapshot = CausalSnapshot(index)
-            for i, (st, en) in enumerate(sparse):
+
+        def enqueue_plan(i):
+            st, en = sparse[i]
+            with torch.cuda.stream(side):
                 pl = fused_chunk_plan(q[st:en], self._query_state(qp[st:en]), index, snapshot, st,
                                       en - 1, temperature=cfg.selection_temperature,
                                       beta=cfg.bucket_size_penalty, target_tokens=self.target_tokens,
@@ -172,12 +176,16 @@ class SembloAttention:
                 nnz_host[i:i + 1].copy_(pl.kv.nnz_d, non_blocking=True)
                 ev = torch.cuda.Event()
                 ev.record(side)
-                plans.append(pl)
-                ready.append(ev)
-            built = torch.cuda.Event()
-            built.record(side)
+            plans.append(pl)
+            ready.append(ev)
+
         self.index = index
-        for i, ((st, en), pl) in enumerate(zip(sparse, plans)):
+        if sparse:
+            enqueue_plan(0)
+        for i, (st, en) in enumerate(sparse):
+            if i + 1 < len(sparse):
+                enqueue_plan(i + 1)
+            pl = plans[i]
             ready[i].synchronize()          # this chunk's partial count is on the host
             main.wait_event(ready[i])
             if i == 0:
@@ -188,6 +196,8 @@ class SembloAttention:
                 t.record_stream(main)
             fused_chunk_execute(pl, q[st:en], index, int(nnz_host[i]),
                                 sm_scale=self.scaling, out=out[st:en], timing=timing)
+        built = torch.cuda.Event()
+        built.record(side)
         # the decode state uses the index on this stream
         main.wait_event(built)
         if not sparse:
