@@ -76,6 +76,18 @@ int sbsa_kmeans_centroids(int mode, const float* sums, const int32_t* counts,
                           const int32_t* row_index, int num_clusters, int dim, float* cent_f32,
                           void* cent_bf16, hipStream_t stream);
 
+/* Iterations it0 .. it1-1 of fit_flat_codebook's k-means loop
+ * (semblo/inference/flat_index.py:264-289) without restarts, in one call:
+ * each is sbsa_kmeans_assign, sbsa_kmeans_update into sums_hist[it] [C, dim]
+ * and counts_hist[it] [C], and sbsa_kmeans_centroids mode 1 with no_restart
+ * (C entries of -1).  The rows are x (bf16 for the assignment, fp32 for the
+ * sums, both with row stride ld_x) at row_index [n]; assign [n] is scratch. */
+int sbsa_kmeans_iterate(const void* x_bf16, const float* x_f32, int64_t ld_x,
+                        const int32_t* row_index, int64_t n, int num_clusters, int dim,
+                        int32_t* assign, float* sums_hist, int32_t* counts_hist,
+                        const int32_t* no_restart, float* cent_f32, void* cent_bf16, int it0,
+                        int it1, hipStream_t stream);
+
 /* Stable counting sort of positions by cluster into page-aligned runs:
  * replaces argsort/bincount + _page_align_order
  * (semblo/vllm_plugin/state.py:850-866, 44-84).  Writes sizes [C], indptr

@@ -687,6 +687,26 @@ int sbsa_kmeans_centroids(int mode, const float* sums, const int32_t* counts,
   return SBSA_OK;
 }
 
+int sbsa_kmeans_iterate(const void* x_bf16, const float* x_f32, int64_t ld_x,
+                        const int32_t* row_index, int64_t n, int num_clusters, int dim,
+                        int32_t* assign, float* sums_hist, int32_t* counts_hist,
+                        const int32_t* no_restart, float* cent_f32, void* cent_bf16, int it0,
+                        int it1, hipStream_t stream) {
+  if (!sums_hist || !counts_hist || !no_restart || it0 < 0 || it1 < it0) return SBSA_ERR_ARG;
+  for (int it = it0; it < it1; ++it) {
+    float* sums = sums_hist + (int64_t)it * num_clusters * dim;
+    int32_t* counts = counts_hist + (int64_t)it * num_clusters;
+    int rc = sbsa_kmeans_assign(x_bf16, ld_x, row_index, n, cent_bf16, num_clusters, dim, assign, stream);
+    if (rc == SBSA_OK)
+      rc = sbsa_kmeans_update(x_f32, ld_x, row_index, n, assign, num_clusters, dim, sums, counts, stream);
+    if (rc == SBSA_OK)
+      rc = sbsa_kmeans_centroids(1, sums, counts, no_restart, x_f32, ld_x, row_index, num_clusters,
+                                 dim, cent_f32, cent_bf16, stream);
+    if (rc != SBSA_OK) return rc;
+  }
+  return SBSA_OK;
+}
+
 size_t sbsa_bucket_layout_workspace_bytes(int64_t length, int num_clusters) {
   int64_t nchunks = (length + LAYOUT_CHUNK - 1) / LAYOUT_CHUNK;
   return (size_t)(nchunks * num_clusters + 64) * sizeof(int32_t);

@@ -181,17 +181,13 @@ class ProductPostingIndex:
             return both[:fit_n], both[fit_n:]
 
         def iterate(start, sample_idx):
-            # k-means steps start.. with no restart rows; an iteration that left a
-            # cluster empty is found afterwards from counts_hist and redone
-            for it in range(start, iters):
-                _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, _lib.ptr(sample_idx),
-                          fit_n, _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_s), s)
-                _lib.call("sbsa_kmeans_update", _lib.ptr(space_f32), index_dim,
-                          _lib.ptr(sample_idx), fit_n, _lib.ptr(assign_s), c, index_dim,
-                          _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]), s)
-                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
-                          _lib.ptr(no_restart), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
-                          c, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+            # k-means steps start.. with no restart rows, in one call; an iteration
+            # that left a cluster empty is found afterwards from counts_hist and redone
+            if start < iters:
+                _lib.call("sbsa_kmeans_iterate", _lib.ptr(space_bf), _lib.ptr(space_f32), index_dim,
+                          _lib.ptr(sample_idx), fit_n, c, index_dim, _lib.ptr(assign_s),
+                          _lib.ptr(sums_hist), _lib.ptr(counts_hist), _lib.ptr(no_restart),
+                          _lib.ptr(cent_f32), _lib.ptr(cent_bf), start, iters, s)
 
         def first_empty(it0):
             """The first iteration >= it0 that left a cluster empty, or -1 (one host read)."""
