@@ -200,9 +200,9 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       if (claimed >= 0) pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
     }
     __syncthreads();
-    const int v = __builtin_amdgcn_readfirstlane(s_item);   // uniform: scalar loads below
-    __syncthreads();
-    return v;
+    // uniform: scalar loads below.  s_item is written again only at the next
+    // claim, after this item's steps, each of which ends with a barrier
+    return __builtin_amdgcn_readfirstlane(s_item);
   };
   // this lane's Q row R = wave*32 + l32 is (query slot R / G, head R % G)
   const int row_i = (wave * 32 + l32) / G, row_j = (wave * 32 + l32) % G;
@@ -639,17 +639,32 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
                             : a.part_lse + (entry0 + row_i) * G + row_j;
         if (ldst) *ldst = lse;
       }
-      // 16-byte chunk c of row r sits at chunk c ^ (r % 32) of the row
+      // 16-byte chunk c of row r sits at chunk c ^ (r % 32) of the row.  Lane
+      // (l32, g) holds dims 32 dt + 8 q4 + 4 g .. +3; a swap between the lane
+      // halves (lanes l and l + 32) gives lane g = 0 all 8 dims of chunk
+      // 4 dt + 2 p and lane g = 1 those of chunk 4 dt + 2 p + 1 (q4 = 2 p, 2 p + 1),
+      // so each lane writes whole 16-byte chunks
       unsigned char* stage = smem_attn + S::stage_offset(PIPE) + wave * 32 * S::ROW_BYTES;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          u32x2_t w;
-          w.x = pack2bf(o[dt][4 * q4 + 0] * inv, o[dt][4 * q4 + 1] * inv);
-          w.y = pack2bf(o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
-          const int c = (4 * dt + q4) ^ (l32 & (S::CH - 1));
-          *reinterpret_cast<u32x2_t*>(stage + l32 * S::ROW_BYTES + 16 * c + 8 * g) = w;
+        for (int p = 0; p < 2; ++p) {
+          const int qa = 2 * p, qb2 = 2 * p + 1;
+          const uint32_t a0 = pack2bf(o[dt][4 * qa + 0] * inv, o[dt][4 * qa + 1] * inv);
+          const uint32_t a1 = pack2bf(o[dt][4 * qa + 2] * inv, o[dt][4 * qa + 3] * inv);
+          const uint32_t b0 = pack2bf(o[dt][4 * qb2 + 0] * inv, o[dt][4 * qb2 + 1] * inv);
+          const uint32_t b1 = pack2bf(o[dt][4 * qb2 + 2] * inv, o[dt][4 * qb2 + 3] * inv);
+          // lanes < 32 keep their q4 = 2p pair and take the upper lanes' one;
+          // lanes >= 32 take the lower lanes' q4 = 2p + 1 pair and keep theirs
+          const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+          u32x4_t w;
+          w.x = s0[0];
+          w.y = s1[0];
+          w.z = s0[1];
+          w.w = s1[1];
+          const int c = (4 * dt + 2 * p + g) ^ (l32 & (S::CH - 1));
+          *reinterpret_cast<u32x4_t*>(stage + l32 * S::ROW_BYTES + 16 * c) = w;
         }
       // read back whole rows (instruction m covers rows ROWS_PER_INST m ..),
       // reads first, then the stores, so no store waits on a single read
