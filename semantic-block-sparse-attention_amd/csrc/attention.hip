@@ -86,6 +86,17 @@ __device__ __forceinline__ void lds_dma4(u32x4_t rsrc, uint32_t lds_addr, uint32
                : "memory", "m0");
 }
 
+// v + (or max with) the same value of lane l ^ 32, in every lane: one swap of
+// the lane halves instead of an LDS permute
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -594,7 +605,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       if (pass == 0) {
         // reference maximum: the row's maximum over the first tile (key 0 of
         // an item is visible to every row, so it is finite)
-        const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
+        const float mx = halves_max(lmax_all);
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
       int t = 0;
@@ -612,11 +623,11 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         if (t + 1 < ntiles) step(t + 1, sB, sA, sweep);
       }
       if (pass == 0) {
-        const float l = l_part + __shfl_xor(l_part, 32, 64);
+        const float l = halves_sum(l_part);
         const bool over = !(l <= __builtin_exp2f(OVERFLOW_LOG2));
         if (!__syncthreads_or(over ? 1 : 0)) break;
       } else if (sweep) {
-        const float mx = fmaxf(lmax_all, __shfl_xor(lmax_all, 32, 64));
+        const float mx = halves_max(lmax_all);
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
     }
@@ -631,7 +642,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     // rows are contiguous in part_o, and the G heads of a query are
     // contiguous in the window output.
     {
-      const float l = l_part + __shfl_xor(l_part, 32, 64);
+      const float l = halves_sum(l_part);
       const float inv = (l > 0.f) ? 1.0f / l : 0.f;
       if (qidx_r >= 0 && g == 0) {
         const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
