@@ -301,9 +301,10 @@ __global__ __launch_bounds__(1024) void rev_scan_kernel(const int32_t* __restric
 // local-window items first (longest first), then cluster items in (head,
 // cluster) order.  Item = {head, cluster or -1, first query slot, query
 // count}.  queue = {n[8], off[8], counter[8]}; the counters are zeroed here.
-// One block: per-XCD counts, each source's first item (a scan per XCD), then
-// every wave expands whole sources (a window tile, or the query tiles of one
-// (head, cluster)) with its 64 lanes.
+// One block: per-XCD counts, each source's first item (one pass of eight
+// per-segment wave scans over each round of 1024 sources), then one thread
+// per source writes its items (a window tile, or the query tiles of one
+// (head, cluster)).
 __device__ __forceinline__ int local_xcd(int h, int tile, int hkv) {
   const int per = hkv >= 8 ? 1 : 8 / hkv;      // XCDs per KV head
   return ((h * per) + (tile % per)) & 7;
@@ -348,9 +349,8 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
                                                            int64_t cap) {
   extern __shared__ int s_first[];     // [nsrc] first item of each source
   __shared__ int cnt[8];
-  __shared__ int off[8];
-  __shared__ int wsum[16];
-  __shared__ int carry;
+  __shared__ int base[8];
+  __shared__ int wsum[16][8];
   const int nloc = has_local ? (Qc + QT - 1) / QT : 0;
   const int nsrc = nloc * hkv + hkv * C;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -364,59 +364,78 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
   if (threadIdx.x == 0) {
     int run = 0;
     for (int x = 0; x < 8; ++x) {
-      off[x] = run;
+      base[x] = run;        // the segment's offset, then its running fill
       run += cnt[x];
     }
   }
   __syncthreads();
-  for (int x = 0; x < 8; ++x) {
-    if (threadIdx.x == 0) carry = off[x];
-    __syncthreads();
-    for (int base = 0; base < nsrc; base += 1024) {
-      const int s = base + threadIdx.x;
-      int n = 0;
-      if (s < nsrc) {
-        const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
-        if (si.x == x) n = si.n;
-      }
-      const int incl = wave_incl_scan(n);
-      if (lane == 63) wsum[wave] = incl;
-      __syncthreads();
-      int o = carry;
-      for (int w = 0; w < wave; ++w) o += wsum[w];
-      if (n) s_first[s] = o + incl - n;
-      __syncthreads();
-      if (threadIdx.x == 1023) carry = o + incl;
-      __syncthreads();
-    }
+  if (threadIdx.x < 8) {
+    const int x = threadIdx.x;
+    const int64_t end = min((int64_t)base[x] + cnt[x], cap);
+    queue[x] = (int32_t)max((int64_t)0, end - base[x]);   // n
+    queue[8 + x] = base[x];                              // offset
+    queue[16 + x] = 0;                                   // counter
   }
-  // expansion: one wave per source
-  for (int s = wave; s < nsrc; s += 16) {
+  // each source's first item: the segment's fill plus the items of the
+  // segment's earlier sources, by one scan per segment over each round of
+  // 1024 sources (sources keep their order within a segment)
+  for (int r0 = 0; r0 < nsrc; r0 += 1024) {
+    const int s = r0 + threadIdx.x;
+    int n = 0, x = 0;
+    if (s < nsrc) {
+      const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+      n = si.n;
+      x = si.x;
+    }
+    int mine = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int incl = wave_incl_scan_dpp(x == k ? n : 0);
+      if (x == k) mine = incl - n;
+      if (lane == 63) wsum[wave][k] = incl;
+    }
+    __syncthreads();
+    if (n) {
+      int o = base[x] + mine;
+      for (int w = 0; w < wave; ++w) o += wsum[w][x];
+      s_first[s] = o;
+    }
+    __syncthreads();
+    if (threadIdx.x < 8) {
+      int t = 0;
+      for (int w = 0; w < 16; ++w) t += wsum[w][threadIdx.x];
+      base[threadIdx.x] += t;
+    }
+    __syncthreads();
+  }
+  // expansion: one thread per source writes its items
+  for (int s = threadIdx.x; s < nsrc; s += 1024) {
     const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
     if (!si.n) continue;
-    const int f0 = s_first[s];
-    for (int j = lane; j < si.n; j += 64) {
-      const int64_t pos = (int64_t)f0 + j;
+    int64_t f0 = s_first[s];
+    int64_t rel = 0;
+    int ent = 0, row = 0, nk = 0;
+    if (si.c >= 0) {
+      nk = nvis[si.h * C + si.c];
+      ent = rev_indptr[si.h * C + si.c];
+      row = indptr[si.h * (C + 1) + si.c];
+    }
+    for (int j = 0; j < si.n; ++j, ++rel) {
+      const int64_t pos = f0 + rel;
       if (pos >= cap) break;
       const int qb = si.c >= 0 ? j * QT : si.qb;
       const int qn = si.c >= 0 ? min(QT, si.qn - qb) : si.qn;
       PrefillItem it{si.h, si.c, qb, qn, 0, 0, 0, 0};
       if (si.c >= 0) {
-        it.nkeys = nvis[si.h * C + si.c];
-        it.entry0 = rev_indptr[si.h * C + si.c] + qb;
-        it.row0 = indptr[si.h * (C + 1) + si.c];
+        it.nkeys = nk;
+        it.entry0 = ent + qb;
+        it.row0 = row;
       }
       items[pos] = it;
     }
   }
-  if (threadIdx.x < 8) {
-    const int x = threadIdx.x;
-    const int64_t end = min((int64_t)off[x] + cnt[x], cap);
-    queue[x] = (int32_t)max((int64_t)0, end - off[x]);   // n
-    queue[8 + x] = off[x];                               // offset
-    queue[16 + x] = 0;                                   // counter
-  }
 }
+
 
 }  // namespace
 
