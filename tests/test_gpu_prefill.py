@@ -86,6 +86,49 @@ def test_sparse_chunk_matches_fp64_over_the_selected_set(cfg):
     print(f"{cfg}: max err {err:.3g}, selection {rep}")
 
 
+@pytest.mark.parametrize("cfg", [dict(hq=16, hkv=4, d=256, grid=8), dict(hq=8, hkv=2, d=128, grid=0)])
+def test_sparse_chunk_redone_when_keys_tower_over_the_first_tile(cfg):
+    """Sparse chunk (the pipelined kernel form): the index is built on ordinary keys,
+    the attention reads keys of which every 97th lies far along the queries' common
+    direction, so items whose cluster run (or window) holds one past its first tile
+    pass 2^64 and are redone with the rows' true maxima.  On a grid of 8 blocks each
+    block works through many items, with the next item's query slots and Q rows
+    staged during the current one.  Exact attention over the selected set."""
+    from semblo_amd.kv_outer import kv_outer_attention
+    from semblo_amd.fused_select import theta_select_bitmask_flat
+    from semblo_amd.state import ProductPostingIndex
+    from semblo_amd.trivial_router import trivial_router_vectors
+    gen = torch.Generator().manual_seed(23)
+    length, hq, hkv, d = 4096, cfg["hq"], cfg["hkv"], cfg["d"]
+    cs, ce = 2048, 3071
+    u = torch.randn(d, generator=gen)
+    q = (3 * u + torch.randn(length, hq, d, generator=gen)).to(torch.bfloat16)
+    k = torch.randn(length, hkv, d, generator=gen).to(torch.bfloat16)
+    v = torch.randn(length, hkv, d, generator=gen).to(torch.bfloat16)
+    k_att = k.clone()
+    k_att[97::97] = (3.0 * u).to(torch.bfloat16)
+    qd, kd, kad, vd = q.to(DEV), k.to(DEV), k_att.to(DEV), v.to(DEV)
+    idx = ProductPostingIndex.build(kd, torch.arange(length, device=DEV), codebook_seed=5,
+                                    router_pass=True)
+    idx.pack_prompt_kv(kad, vd)
+    c = idx.bucket_sizes.shape[1]
+    qc = qd[cs:ce + 1]
+    qn = qc.shape[0]
+    sizes = idx.causal_sizes(cs)
+    vec = trivial_router_vectors(qc, 1)
+    qmask = torch.empty(qn, hkv, c // 32, dtype=torch.int32, device=DEV)
+    theta_select_bitmask_flat(vec.view(qn, hq, 1, d), None, idx.codebooks, sizes[None], None,
+                              temperature=0.1, beta=0.25, target_tokens=length // 16, g_union=32,
+                              qmask=qmask)
+    out, _ = kv_outer_attention(qc, idx.packed_kv, qmask, sizes, idx.bucket_indptr,
+                                sm_scale=d ** -0.5, local_kv=(kad[cs:ce + 1], vd[cs:ce + 1]),
+                                chunk_start=cs, wstart=cs, grid=cfg["grid"] or None)
+    torch.cuda.synchronize()
+    want = _reference_sparse(idx, q, k_att, v, cs, ce, qmask.cpu(), sizes.cpu())
+    err = assert_close_bf16(out.cpu(), want, f"towering keys, sparse chunk {cfg}")
+    print(f"{cfg}: max err {err:.3g}")
+
+
 @pytest.mark.parametrize("cfg", [dict(length=2048, hq=8, hkv=2, d=128, cs=0, ce=1023),
                                  dict(length=2048, hq=16, hkv=4, d=256, cs=512, ce=1300)])
 def test_dense_prefix_chunk_is_exact_causal_attention(cfg):
