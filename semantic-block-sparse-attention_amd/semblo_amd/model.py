@@ -87,6 +87,17 @@ class SembloAttention:
             self._side_stream = st
         return st
 
+    def _pinned_counts(self, n: int) -> torch.Tensor:
+        """Pinned host slots for the sparse chunks' partial counts, kept across
+        calls: a pinned allocation per call can stall the host while earlier
+        copies are still pending.  A call reads each slot only after its own
+        copy has landed."""
+        buf = getattr(self, "_nnz_host", None)
+        if buf is None or buf.numel() < max(n, 1):
+            buf = torch.empty(max(n, 64), dtype=torch.int64, pin_memory=True)
+            self._nnz_host = buf
+        return buf
+
     def begin_token_outer_prefill(self, tokens: int, chunk: int, **kw):
         """A token-order prefill session of ``tokens`` positions in slices of ``chunk``
         (the reference's layer.begin_token_outer_prefill, streamed_prefill.py:563-564)."""
@@ -160,7 +171,7 @@ class SembloAttention:
         # an event.  Plans are enqueued one chunk ahead of the attention: a
         # chunk's attention starts as soon as its own plan is done, and the
         # next plan runs beside it.
-        nnz_host = torch.empty(max(len(sparse), 1), dtype=torch.int64, pin_memory=True)
+        nnz_host = self._pinned_counts(len(sparse))
         plans, ready = [], []
         with torch.cuda.stream(side):
             index = self._ingest_prompt_kv(kp, kk, vv)

@@ -43,6 +43,14 @@ class _DrawBuffers:
         self.sub = torch.empty(fit_n, dtype=torch.int64)
         self.pinned = torch.empty(fit_n + c, dtype=torch.int32, pin_memory=True)
         self.uploaded = None            # event after the last upload from `pinned`
+        self.counts = None              # pinned [iterations, C] cluster counts
+
+    def counts_host(self, iters: int, c: int) -> torch.Tensor:
+        """Pinned host copy of the iterations' cluster counts (read after a stream
+        synchronisation, so one buffer serves every build of this shape)."""
+        if self.counts is None or self.counts.shape[0] < iters:
+            self.counts = torch.empty(iters, c, dtype=torch.int32, pin_memory=True)
+        return self.counts[:iters]
 
 
 _DRAW_BUFFERS: dict = {}
@@ -150,7 +158,6 @@ class ProductPostingIndex:
         n_it = max(iters, 1)
         sums_hist = torch.empty(n_it, c, index_dim, dtype=torch.float32, device=dev)
         counts_hist = torch.empty(n_it, c, dtype=torch.int32, device=dev)
-        counts_host = torch.empty(n_it, c, dtype=torch.int32, pin_memory=True)
         no_restart = torch.full((c,), -1, dtype=torch.int32, device=dev)
         assign_s = torch.empty(fit_n, dtype=torch.int32, device=dev)
         assign_all = torch.empty(length, dtype=torch.int32, device=dev)
@@ -165,6 +172,7 @@ class ProductPostingIndex:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
         host = _draw_buffers(length, fit_n, c)
+        counts_host = host.counts_host(n_it, c)
 
         def draw_sample_and_init():
             # fit_flat_codebook's first two draws (flat_index.py:237-262)
