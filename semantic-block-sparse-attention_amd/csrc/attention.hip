@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   constexpr int KS = D / 16;        // 16-dim steps of S^T
   constexpr int DT = D / 32;        // 32-dim tiles of O^T
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
-  __shared__ int s_item;
+  __shared__ int s_items[2];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar LDS bases
@@ -195,25 +195,33 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   int pend = 0;
   if (threadIdx.x == 0) pend = atomicAdd(&a.queue[16 + home], 1);
   __syncthreads();
-  auto next_index = [&]() -> int {
-    if (threadIdx.x == 0) {
-      int claimed = -1;
-      for (;;) {
-        const int x = (home + probe) & 7;
-        if (pend < s_queue[x]) {
-          claimed = s_queue[8 + x] + pend;
-          break;
-        }
-        if (++probe == 8) break;
-        pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
+  // thread 0 only: the next item of this block's queue (stealing from the
+  // other XCDs' queues once it is empty), -1 when every queue is
+  auto claim = [&]() -> int {
+    int claimed = -1;
+    for (;;) {
+      const int x = (home + probe) & 7;
+      if (pend < s_queue[x]) {
+        claimed = s_queue[8 + x] + pend;
+        break;
       }
-      s_item = claimed;
-      if (claimed >= 0) pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
+      if (++probe == 8) break;
+      pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
     }
-    __syncthreads();
-    // uniform: scalar loads below.  s_item is written again only at the next
-    // claim, after this item's steps, each of which ends with a barrier
-    return __builtin_amdgcn_readfirstlane(s_item);
+    if (claimed >= 0) pend = atomicAdd(&a.queue[16 + ((home + probe) & 7)], 1);
+    return claimed;
+  };
+  // Claims run two items ahead through two LDS slots, so reading one needs no
+  // barrier: when an item starts, the next item's index (slot of parity i + 1)
+  // was written when the previous item started, and every item's steps end
+  // with barriers; thread 0 then writes the index after next into the slot
+  // the current item's index came from, which every thread read one item ago.
+  int parity = 0;
+  auto next_index = [&]() -> int {
+    const int v = __builtin_amdgcn_readfirstlane(s_items[parity ^ 1]);   // uniform: scalar loads below
+    if (threadIdx.x == 0) s_items[parity] = v >= 0 ? claim() : -1;
+    parity ^= 1;
+    return v;
   };
   // this lane's Q row R = wave*32 + l32 is (query slot R / G, head R % G)
   const int row_i = (wave * 32 + l32) / G, row_j = (wave * 32 + l32) % G;
@@ -321,7 +329,12 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   };
 
   PrefillItem rec{};
-  int idx = next_index();
+  if (threadIdx.x == 0) {
+    s_items[0] = claim();
+    s_items[1] = s_items[0] >= 0 ? claim() : -1;
+  }
+  __syncthreads();
+  int idx = __builtin_amdgcn_readfirstlane(s_items[0]);
   if (idx >= 0) {
     rec = a.items[idx];
     fetch_slots(rec);
