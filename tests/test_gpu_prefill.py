@@ -70,6 +70,8 @@ def _reference_sparse(idx, q, k, v, cs, ce, qmask, sizes):
     dict(length=2048, hq=16, hkv=4, d=256, cs=1024, ce=1535, seed=2),
     dict(length=4096, hq=16, hkv=4, d=256, cs=3000, ce=3299, seed=3),     # ragged chunk
     dict(length=3000, hq=4, hkv=4, d=128, cs=1900, ce=2999, seed=4),      # G = 1, odd length
+    dict(length=3072, hq=16, hkv=2, d=128, cs=2048, ce=3071, seed=5),     # G = 8
+    dict(length=2048, hq=8, hkv=4, d=256, cs=1024, ce=1700, seed=6),      # G = 2, D = 256
 ])
 def test_sparse_chunk_matches_fp64_over_the_selected_set(cfg):
     inp, q, k, v, idx = _setup(cfg["length"], cfg["hq"], cfg["hkv"], cfg["d"], cfg["seed"])
