@@ -55,7 +55,9 @@ def _csr_to_sel(csr, idx):
 
 
 @pytest.mark.parametrize("cfg", [dict(length=4096, hq=16, hkv=4, d=256, seed=1),
-                                 dict(length=3000, hq=8, hkv=2, d=128, seed=2)])
+                                 dict(length=3000, hq=8, hkv=2, d=128, seed=2),
+                                 dict(length=2048, hq=8, hkv=1, d=128, seed=3),      # G = 8
+                                 dict(length=2048, hq=4, hkv=4, d=256, seed=4)])     # G = 1
 def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
     from semblo_amd.fused_decode import fused_decode_step
     from semblo_amd.synthetic import decode_queries

@@ -132,7 +132,9 @@ def test_sparse_chunk_redone_when_keys_tower_over_the_first_tile(cfg):
 
 
 @pytest.mark.parametrize("cfg", [dict(length=2048, hq=8, hkv=2, d=128, cs=0, ce=1023),
-                                 dict(length=2048, hq=16, hkv=4, d=256, cs=512, ce=1300)])
+                                 dict(length=2048, hq=16, hkv=4, d=256, cs=512, ce=1300),
+                                 dict(length=2048, hq=8, hkv=1, d=128, cs=1024, ce=1535),   # G = 8
+                                 dict(length=1536, hq=4, hkv=4, d=256, cs=700, ce=1300)])   # G = 1
 def test_dense_prefix_chunk_is_exact_causal_attention(cfg):
     from semblo_amd.kv_outer import dense_causal_attention
     from semblo_amd.synthetic import mixture_layer
