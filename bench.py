@@ -17,8 +17,8 @@ graph is replayed: ``decode_us_per_step``.
 
 ``roofline`` is for the dominant kernel, the MFMA attention of the prefill:
 algorithmic FLOPs (4 D per selected key per query head, plus the causal window
-and the dense chunks) over its summed launch time from HIP events on its own
-stream.  ``decode_roofline`` is the decode step's algorithmic bytes over the
+and the dense chunks, counted in one extra pass) over its summed launch time from
+HIP events around every launch of the timed steps, on the stream it runs on.  ``decode_roofline`` is the decode step's algorithmic bytes over the
 per-step graph time.  ``cpu_baseline`` times the oracle's torch CPU path on a
 bounded sample of the same layer (see ``cpu_baseline`` below).
 """
@@ -239,26 +239,30 @@ def main():
             _log(f"warm-up {i} done")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        # events between the steps only log the spread; nothing waits on them
+        # events between the steps only log the spread, and events around every
+        # attention launch time the kernel over the timed steps; nothing waits on them
         marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+        timed = KernelTiming(counts_flops=False)
         marks[0].record()
         for i in range(args.steps):
-            run_prefill(layer, inp, conf)
+            run_prefill(layer, inp, conf, timing=timed)
             marks[i + 1].record()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / max(args.steps, 1)
         per_step = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
         _log(f"prefill {ms:.2f} ms/layer (steps on the GPU clock: {', '.join(f'{x:.1f}' for x in per_step)})")
-        # one instrumented pass: attention kernel time and FLOPs, and the build time
+        # one more pass counts the FLOPs of every launch (the same inputs give the
+        # same FLOPs in every step) and times the store kernels of a token-order prefill
         timing = KernelTiming()
         store = KernelTiming() if conf.get("order") == "token" else None
         run_prefill(layer, inp, conf, timing=timing, store_timing=store)
         torch.cuda.synchronize()
-        attn_ms = timing.total_ms()
+        attn_ms = timed.total_ms() / max(args.steps, 1)
         flops = timing.total_flops()
         achieved = flops / (attn_ms * 1e-3) / 1e12
         result.update(prefill_ms=ms, attn_ms=attn_ms, flops=flops, achieved=achieved,
                       launches=timing.launches())
+        assert timed.launches() == timing.launches() * max(args.steps, 1)
         _log(f"attention kernel {attn_ms:.2f} ms over {timing.launches()} launches, "
              f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s")
         if store is not None:

@@ -107,7 +107,7 @@ def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int,
     q_count, hq, d = q_chunk.shape
     hkv = index.num_kv_heads
     wstart, chunk_start, chunk_end = plan.wstart, plan.chunk_start, plan.chunk_end
-    if timing is not None:
+    if timing is not None and timing.counts_flops:
         # selected rows of every (query, KV head), each read by its G query heads,
         # plus the causal window (p - chunk_start + 1 keys per query and head)
         g = hq // hkv

@@ -203,11 +203,14 @@ class KernelTiming:
     """HIP events around each launch of the attention kernel, on the stream it runs on.
 
     ``begin``/``end`` bracket one launch; ``flops`` collects the algorithmic
-    FLOPs of each launch as device scalars (summed once, at read-out)."""
+    FLOPs of each launch as device scalars (summed once, at read-out).  With
+    ``counts_flops`` false only the events are recorded: nothing but event
+    records is added to the stream, so the timing can run inside a timed region."""
 
-    def __init__(self) -> None:
+    def __init__(self, counts_flops: bool = True) -> None:
         self.events: list[tuple] = []
         self.flops: list = []
+        self.counts_flops = counts_flops
 
     def begin(self, stream_handle: int) -> None:
         # the kernels launch on torch's current stream (the handle passed to libsbsa)
@@ -222,7 +225,8 @@ class KernelTiming:
         self.events[-1][1] = ev
 
     def add_flops(self, value) -> None:
-        self.flops.append(value)
+        if self.counts_flops:
+            self.flops.append(value)
 
     def launches(self) -> int:
         return len(self.events)
