@@ -744,8 +744,9 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
 #undef SBSA_ATT
   if (rc) return rc;
   if (csr_out) {
-    hipMemcpyAsync(csr_out, workspace, ((size_t)3 * num_kv_heads * C + 2 * num_kv_heads) * 4,
-                   hipMemcpyDeviceToDevice, stream);
+    if (hipMemcpyAsync(csr_out, workspace, ((size_t)3 * num_kv_heads * C + 2 * num_kv_heads) * 4,
+                       hipMemcpyDeviceToDevice, stream) != hipSuccess)
+      return SBSA_ERR_LAUNCH;
   }
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;

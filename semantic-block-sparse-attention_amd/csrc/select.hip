@@ -490,12 +490,11 @@ int sbsa_score_select(const void* vectors, int64_t v_sq, int64_t v_sh, const flo
   size_t lds = (size_t)R * (dim + 8) * 2 + (size_t)R * (C + 1) * 4;
   if (lds > 160 * 1024) return SBSA_ERR_UNSUPPORTED;
   if (lds > 64 * 1024) {
-    hipFuncSetAttribute((const void*)score_select_kernel<64>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipFuncSetAttribute((const void*)score_select_kernel<128>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipFuncSetAttribute((const void*)score_select_kernel<256>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const void* fns[3] = {(const void*)score_select_kernel<64>, (const void*)score_select_kernel<128>,
+                          (const void*)score_select_kernel<256>};
+    for (const void* fn : fns)
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return SBSA_ERR_UNSUPPORTED;
   }
   switch (dim) {
     case 64:

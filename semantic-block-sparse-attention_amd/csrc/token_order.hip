@@ -435,8 +435,9 @@ int sbsa_append_rows(const int32_t* ids, int64_t n, int num_kv_heads, int num_cl
   if (num_clusters < 1 || num_clusters > 1024) return SBSA_ERR_UNSUPPORTED;
   if (n > INT32_MAX) return SBSA_ERR_UNSUPPORTED;
   const size_t lds = (size_t)(AR_WAVES + 1) * num_clusters * sizeof(int);
-  hipFuncSetAttribute((const void*)append_rows_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                      (int)lds);
+  if (hipFuncSetAttribute((const void*)append_rows_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return SBSA_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(append_rows_kernel, dim3(num_kv_heads), dim3(64 * AR_WAVES), lds, stream, ids, n,
                      num_clusters, indptr, sizes, reserve, rows, counts, overflow);
   SBSA_CHECK_LAUNCH();
