@@ -60,3 +60,21 @@ def test_product_path_refuses_cpu_tensors():
         pytest.skip("libsbsa.so is not built here")
     with pytest.raises(RuntimeError):
         trivial_router_vectors(torch.randn(4, 2, 64).to(torch.bfloat16))
+
+
+def test_entry_points_reject_bad_arguments_before_any_launch():
+    """Argument checks return SBSA_ERR_ARG (1) before any launch, so they run
+    here without a GPU (the pointers below are never dereferenced)."""
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    lib = _lib.load()
+    p = 256                                   # stand-in for a device pointer
+    # k-means iterations it0..it1 with it1 < it0
+    assert lib.sbsa_kmeans_iterate(p, p, 256, p, 100, 64, 256, p, p, p, p, p, p, 3, 2, None) == 1
+    # the work list without the reverse index's arrays
+    assert lib.sbsa_prefill_items(p, 4, 64, 128, 32, 1, None, p, p, p, 100, p, None) == 1
+    # a window that starts after the chunk
+    assert lib.sbsa_prefill_attend(p, 4096, 256, 128, 16, 4, 256, p, 1024, p, p, 1024, 256, p, p,
+                                   64, p, p, p, p, p, p, p, 4096, 256, p, 512, 1024, 0.0625, 0,
+                                   None) == 1
