@@ -710,7 +710,8 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           const int i = RR / G, j = RR % G;
           bf16_t* dst = local ? a.local_o + (int64_t)(qb + i) * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh
                               : a.part_o + ((entry0 + i) * G + j) * D;
-          if (i < qn) *reinterpret_cast<u32x4_t*>(dst + 8 * c16) = rows[mm];
+          // read once, later, by the combine: kept out of the way of the K/V in L2
+          if (i < qn) __builtin_nontemporal_store(rows[mm], reinterpret_cast<u32x4_t*>(dst + 8 * c16));
         }
       }
     }
