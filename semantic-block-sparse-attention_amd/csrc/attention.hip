@@ -841,7 +841,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
       w.y = pack2bf(acc[8 * k + 2] * inv, acc[8 * k + 3] * inv);
       w.z = pack2bf(acc[8 * k + 4] * inv, acc[8 * k + 5] * inv);
       w.w = pack2bf(acc[8 * k + 6] * inv, acc[8 * k + 7] * inv);
-      *reinterpret_cast<u32x4_t*>(dst + 8 * k) = w;
+      __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(dst + 8 * k));
     }
   } else {
 #pragma unroll
