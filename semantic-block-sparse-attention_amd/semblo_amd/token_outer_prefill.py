@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import os
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -54,17 +55,22 @@ def reserved_layout(sizes_ref: torch.Tensor, n_ref: int, total_tokens: int, widt
     ``width``.
     """
     align = max(int(align), 1)
-    share = sizes_ref.detach().to("cpu", torch.float64) * (float(total_tokens) / float(max(int(n_ref), 1)))
-    rows = torch.ceil(share / align).to(torch.int64).clamp_min(1) * align
-    for h in range(rows.shape[0]):
-        spare = int(width) - int(rows[h].sum())
-        if spare < 0:
-            raise RuntimeError(f"the reserved layout needs {int(rows[h].sum())} rows for KV head {h}; "
-                               f"the store holds {width}")
-        if spare >= align:
-            frac = share[h] / max(float(share[h].sum()), 1.0)
-            rows[h] += torch.floor(frac * (spare // align)).to(torch.int64) * align
-    return rows
+    # This runs between a host read and the repack it decides, while the GPU waits,
+    # so it is a few whole-array operations over every KV head at once: elementwise
+    # float64 in numpy (exact, like torch's), row sums in torch (its summation order).
+    share_t = sizes_ref.detach().to("cpu", torch.float64) * (float(total_tokens) / float(max(int(n_ref), 1)))
+    share = share_t.numpy()
+    rows = np.maximum(np.ceil(share / align).astype(np.int64), 1) * align
+    need = rows.sum(1)
+    spare = int(width) - need
+    if (spare < 0).any():
+        h = int(np.flatnonzero(spare < 0)[0])
+        raise RuntimeError(f"the reserved layout needs {int(need[h])} rows for KV head {h}; "
+                           f"the store holds {width}")
+    total = np.maximum(share_t.sum(1, keepdim=True).numpy(), 1.0)
+    extra = np.floor((share / total) * (spare // align)[:, None].astype(np.float64)).astype(np.int64) * align
+    rows += np.where((spare >= align)[:, None], extra, 0)
+    return torch.from_numpy(rows)
 
 
 def nearest_cluster(keys: torch.Tensor, codebooks: torch.Tensor, *, router_pass: bool = True,
