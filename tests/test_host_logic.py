@@ -1,0 +1,44 @@
+"""Host-side logic of the product path that runs without a GPU, checked against the oracle."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.reference_cpu as ref
+from semblo_amd.token_outer_prefill import reserved_layout
+
+
+def _layout_or_none(fn, *args):
+    try:
+        return fn(*args)
+    except RuntimeError:
+        return None
+
+
+@pytest.mark.parametrize("align", [1, 16, 64])
+def test_reserved_layout_matches_the_oracle_bit_for_bit(align):
+    """The host computes every KV head's layout in whole-array arithmetic; the runs
+    must come out exactly as the oracle's per-head restatement lays them out
+    (token_outer_prefill.py:39-63), and refuse the same stores."""
+    g = torch.Generator().manual_seed(align)
+    refused = 0
+    for t in range(300):
+        hkv = int(torch.randint(1, 9, (1,), generator=g))
+        c = int(torch.randint(3, 600, (1,), generator=g))
+        if t % 3 == 0:
+            sizes = torch.randint(0, 3000, (hkv, c), generator=g)
+        elif t % 3 == 1:                         # a few large clusters, many tiny ones
+            sizes = (torch.rand(hkv, c, generator=g) ** 8 * 5000).long()
+        else:                                    # nearly every cluster empty
+            sizes = torch.zeros(hkv, c, dtype=torch.long)
+            sizes[:, :3] = torch.randint(0, 99999, (hkv, 3), generator=g)
+        n = int(sizes.sum(1).max()) + int(torch.randint(0, 50, (1,), generator=g))
+        total = n * int(torch.randint(1, 8, (1,), generator=g)) + int(torch.randint(0, 1000, (1,), generator=g))
+        width = total + c * align + int(torch.randint(-3000, 5000, (1,), generator=g))
+        want = _layout_or_none(ref.reserved_layout, sizes, n, total, width, align)
+        got = _layout_or_none(reserved_layout, sizes, n, total, width, align)
+        refused += want is None
+        assert (want is None) == (got is None), (t, hkv, c, width)
+        if want is not None:
+            assert got.dtype == torch.int64 and torch.equal(got, want), (t, hkv, c, width)
+    assert 0 < refused < 300          # both outcomes were exercised
