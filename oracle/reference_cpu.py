@@ -132,14 +132,16 @@ def segment_sum_matmul(x: torch.Tensor, assign: torch.Tensor, num_clusters: int,
 
 def fit_flat_codebook(space: torch.Tensor, num_clusters: int, *, num_iters: int,
                       sample_size: int, generator: torch.Generator,
-                      chunk: int = 65536, trace: list | None = None) -> torch.Tensor:
+                      chunk: int = 65536, trace: list | None = None,
+                      steps: list | None = None) -> torch.Tensor:
     """flat_index.py:193-289 with init="random", metric="cosine", deterministic sums.
 
     ``space`` is already unit-norm fp32 (routing_space), so _fit_space's
     F.normalize is applied again exactly as the reference does.  ``trace``, if
     given, receives the random draws (sample rows, init rows, and per iteration
     the replacement rows of empty clusters) so a device implementation can be
-    fed the identical draws.
+    fed the identical draws.  ``steps``, if given, receives per iteration the
+    fp32 centroids it starts from, its assignment, counts and sums.
     """
     x = F.normalize(space.float(), dim=-1)
     n = x.shape[0]
@@ -154,9 +156,13 @@ def fit_flat_codebook(space: torch.Tensor, num_clusters: int, *, num_iters: int,
         trace.append(("sample", perm[:fit_n].clone()))
         trace.append(("init", init.clone()))
     for _ in range(num_iters):
+        if steps is not None:
+            steps.append(dict(entry=centroids.clone()))
         assign = argmax_sim_chunked(sample, centroids, chunk)
         counts = torch.bincount(assign, minlength=num_clusters)
         sums = segment_sum_matmul(sample, assign, num_clusters)
+        if steps is not None:
+            steps[-1].update(assign=assign.clone(), counts=counts.clone(), sums=sums.clone())
         empty = counts == 0
         if bool(empty.any()):
             repl = torch.randperm(fit_n, generator=generator)[: int(empty.sum())]
@@ -199,7 +205,8 @@ def build_flat_index(product_keys: torch.Tensor, positions: torch.Tensor | None 
                      unit_tokens: int = 2048, min_clusters_log2: int = 7,
                      sample_size: int = 8192, fit_iters: int = 8, per_centroid: int = 32,
                      codebook_seed: int = 0, page_align: int = 16,
-                     num_clusters: int | None = None, traces: list | None = None) -> dict:
+                     num_clusters: int | None = None, traces: list | None = None,
+                     fit_steps: list | None = None) -> dict:
     """ProductPostingIndex._build_flat, state.py:545-948, on the paper path.
 
     product_keys [L, Hkv, I] are the router's output (routing_normalize_keys of
@@ -220,11 +227,14 @@ def build_flat_index(product_keys: torch.Tensor, positions: torch.Tensor | None 
         space = routing_space(keys)
         fit_sample = min(length, max(int(sample_size), per_centroid * c))
         trace = [] if traces is not None else None
+        steps = [] if fit_steps is not None else None
         cents = fit_flat_codebook(space, c, num_iters=fit_iters, sample_size=fit_sample,
-                                  generator=gen, trace=trace)
+                                  generator=gen, trace=trace, steps=steps)
         if traces is not None:
             traces.append(trace)
         assign = argmax_sim_chunked(F.normalize(space.float(), dim=-1), cents, 65536)
+        if fit_steps is not None:
+            fit_steps.append(dict(steps=steps, final_centroids=cents, final_assign=assign))
         order = torch.argsort(assign, stable=True)
         counts = torch.bincount(assign, minlength=c).to(torch.int32)
         if page_align > 1:
@@ -494,17 +504,20 @@ def lse_merge(o_a, lse_a, o_b, lse_b):
 
 def decode_reference(q: torch.Tensor, packed: torch.Tensor, indptr: torch.Tensor,
                      sizes: torch.Tensor, sel: torch.Tensor, suffix_k: torch.Tensor,
-                     suffix_v: torch.Tensor, sm_scale: float) -> torch.Tensor:
+                     suffix_v: torch.Tensor, sm_scale: float, with_lse: bool = False):
     """fp64 attention of one decode query over the selected clusters' full runs
     plus the visible suffix (tests/test_fused_decode_v3.py:98-124 of the reference).
 
     q [Hq, D]; packed [2, W, Hkv, D]; sel [Hkv, C] bool; suffix_k/v [S, Hkv, D]
-    are the suffix tokens at positions <= the query's.
+    are the suffix tokens at positions <= the query's.  With ``with_lse`` also
+    returns the natural-log log-sum-exp of the scaled scores [Hq]
+    (fused_prefill.py:625-718 returns it beside the output).
     """
     hq, d = q.shape
     hkv = packed.shape[2]
     g = hq // hkv
     out = torch.zeros(hq, d, dtype=torch.float64)
+    lse = torch.full((hq,), -math.inf, dtype=torch.float64)
     for h in range(hkv):
         rows = [torch.arange(int(indptr[h, cl]), int(indptr[h, cl]) + int(sizes[h, cl]))
                 for cl in torch.nonzero(sel[h]).flatten().tolist()]
@@ -514,7 +527,9 @@ def decode_reference(q: torch.Tensor, packed: torch.Tensor, indptr: torch.Tensor
         for t in range(g):
             s = (kk @ q[h * g + t].double()) * sm_scale
             out[h * g + t] = torch.softmax(s, dim=0) @ vv
-    return out
+            if s.numel():
+                lse[h * g + t] = torch.logsumexp(s, dim=0)
+    return (out, lse) if with_lse else out
 
 
 # ---------------------------------------------------------------- S10 ---------

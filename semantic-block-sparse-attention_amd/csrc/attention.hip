@@ -943,6 +943,14 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads) return SBSA_ERR_ARG;
   if (q_sq % 8 || q_sh % 8 || o_st % 8 || o_sh % 8 || lo_sq % 4 || lo_sh % 4) return SBSA_ERR_ARG;
   if (chunk_start < wstart || wstart < 0) return SBSA_ERR_ARG;
+  // The tile loads address K/V through raw buffer resources whose range (the rows
+  // left from a tile's first row, in bytes) is 32-bit: the longest row range a work
+  // item can read, the window from wstart to the chunk's last query or a whole packed
+  // run, must stay below 4 GiB.
+  const int64_t window_bytes = (chunk_start + num_queries - wstart) * o_st * 2;
+  const int64_t packed_bytes = packed ? packed_len * num_kv_heads * (int64_t)dim * 2 : 0;
+  if (window_bytes >= (int64_t(1) << 32) || packed_bytes >= (int64_t(1) << 32))
+    return SBSA_ERR_UNSUPPORTED;
   AttnArgs a;
   a.q = (const bf16_t*)q;
   a.q_sq = q_sq;
@@ -987,6 +995,12 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
   if (!qmask || !nvis || !rev_indptr || !qrank || !local_o || !local_lse || !out) return SBSA_ERR_ARG;
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_clusters % 32) return SBSA_ERR_ARG;
   if (num_clusters > COMBINE_MAX_LIST) return SBSA_ERR_UNSUPPORTED;
+  // rows are read and written in 16-byte pieces when a lane's share of a head is a
+  // multiple of 8 values: every row start must then be 16-byte aligned
+  if ((num_q_heads / num_kv_heads) * dim % 512 == 0 &&
+      (out_sq % 8 || out_sh % 8 || lo_sq % 8 || lo_sh % 8 || ((uintptr_t)out & 15) ||
+       ((uintptr_t)local_o & 15)))
+    return SBSA_ERR_ARG;
   if (num_queries == 0) return SBSA_OK;
   int rc = combine_dispatch(dim, num_q_heads / num_kv_heads, qmask, nvis, rev_indptr, qrank,
                             (const bf16_t*)part_o, part_lse, (const bf16_t*)local_o, lo_sq, lo_sh,

@@ -103,8 +103,11 @@ class _PromptOnly:
 
 def decode_prompt_only(q_chunk: torch.Tensor, vectors: torch.Tensor, index, *, temperature: float,
                        beta: float, target_tokens: int, sm_scale: float, iters: int = 16,
-                       num_splits: int = 64) -> PagedSparseAttentionResult:
-    """fused_decode_attention's contract: [1, Hq, D] out and [1, Hq] LSE over the prompt."""
+                       num_splits: int = 64,
+                       csr_out: torch.Tensor | None = None) -> PagedSparseAttentionResult:
+    """fused_decode_attention's contract: [1, Hq, D] out and [1, Hq] LSE over the prompt.
+    ``csr_out`` (int32, 3 Hkv C + 2 Hkv) receives the step's selected runs, as in
+    fused_decode_step."""
     hq, d = q_chunk.shape[1], q_chunk.shape[2]
     hkv = index.num_kv_heads
     dev = q_chunk.device
@@ -122,5 +125,5 @@ def decode_prompt_only(q_chunk: torch.Tensor, vectors: torch.Tensor, index, *, t
               256, _lib.ptr(holder.suffix_table), holder.prompt_length, holder.max_tiles, hq, hkv,
               index.num_buckets, d, 1.0 / float(temperature), float(beta), float(target_tokens),
               int(iters), 0, float(sm_scale), int(num_splits), 1, _lib.ptr(ws.buffer), ws.nbytes,
-              _lib.ptr(out), d, _lib.ptr(lse), None, _lib.stream(dev))
+              _lib.ptr(out), d, _lib.ptr(lse), _lib.ptr(csr_out), _lib.stream(dev))
     return PagedSparseAttentionResult(output=out, logsumexp=lse)

@@ -54,9 +54,18 @@ class ChunkPlan:
     """The selection side of one sparse chunk: its causal snapshot, the per-query
     cluster masks and the reverse index, all on the device."""
 
-    def __init__(self, chunk_start, chunk_end, wstart, causal_sizes, tokens, kv):
+    def __init__(self, chunk_start, chunk_end, wstart, causal_sizes, tokens, kv, theta=None):
         self.chunk_start, self.chunk_end, self.wstart = chunk_start, chunk_end, wstart
         self.causal_sizes, self.tokens, self.kv = causal_sizes, tokens, kv
+        self.theta = theta
+
+    def record(self, log: list | None) -> None:
+        """Append what decided this chunk's key sets to ``log`` (a test hook: the per-query
+        cluster masks, the causal sizes and the cut theta, device tensors)."""
+        if log is not None:
+            log.append(dict(chunk_start=self.chunk_start, chunk_end=self.chunk_end,
+                            wstart=self.wstart, causal_sizes=self.causal_sizes,
+                            qmask=self.kv.qmask, theta=self.theta))
 
     def tensors(self):
         kv = self.kv
@@ -75,9 +84,10 @@ def chunk_window_start(chunk_start: int, target_tokens: int, dense_prefix_x: int
 def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, chunk_start: int,
                      chunk_end: int, *, temperature: float, beta: float, target_tokens: int,
                      queries_per_block: int = 32, iters: int = 16, local: int = 0,
-                     dense_prefix_x: int = 4) -> ChunkPlan:
+                     dense_prefix_x: int = 4, keep_theta: bool = False) -> ChunkPlan:
     """Selection and reverse index of a sparse chunk (fused_prefill.py:281-482 up to
-    the attention calls); no host read."""
+    the attention calls); no host read.  ``keep_theta`` also keeps each query's cut
+    (for ChunkPlan.record)."""
     q_count = q_chunk.shape[0]
     hkv = index.num_kv_heads
     c = index.num_buckets
@@ -92,12 +102,13 @@ def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, 
     nb = (q_count + g_union - 1) // g_union
     bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
     qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
+    theta = torch.empty(q_count, hkv, dtype=torch.float32, device=q_chunk.device) if keep_theta else None
     _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None],
                                           bitmask, temperature=temperature, beta=beta,
                                           target_tokens=target_tokens, g_union=g_union,
-                                          iters=iters, qmask=qmask)
+                                          iters=iters, qmask=qmask, theta_out=theta)
     kv = kv_outer_plan(qmask, causal_sizes, num_queries=q_count)
-    return ChunkPlan(chunk_start, chunk_end, wstart, causal_sizes, tokens, kv)
+    return ChunkPlan(chunk_start, chunk_end, wstart, causal_sizes, tokens, kv, theta)
 
 
 def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int, *, sm_scale: float,
@@ -135,7 +146,8 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
                           queries_per_block: int = 32, sm_scale: float, iters: int = 16,
                           fa3_page_size: int = 16, kv_outer_default: bool = True,
                           dense_prefix_x: int = 4, local: int = 0, out: torch.Tensor | None = None,
-                          timing=None, window_kv=None, **unused) -> torch.Tensor:
+                          timing=None, window_kv=None, plan_log: list | None = None,
+                          **unused) -> torch.Tensor:
     """Attention of one query chunk [chunk_start, chunk_end] (fused_prefill.py:219-482).
 
     While chunk_start <= dense_prefix_x * K the chunk is dense and causal over
@@ -145,6 +157,7 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     rows wstart..chunk_end in prompt order, replaces the slice of
     ``index.original_kv`` for that window (the token-order prefill, whose
     store has no prompt-order copy).  One host read (the partial count).
+    ``plan_log``: a test hook, see ChunkPlan.record.
     """
     if not kv_outer_default or not fa3_page_size:
         raise NotImplementedError("only the paper path (FA3 page body, KV-outer) is built")
@@ -166,7 +179,8 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     plan = fused_chunk_plan(q_chunk, query_state, index, snapshot_state, chunk_start, chunk_end,
                             temperature=temperature, beta=beta, target_tokens=target_tokens,
                             queries_per_block=queries_per_block, iters=iters, local=local,
-                            dense_prefix_x=dense_prefix_x)
+                            dense_prefix_x=dense_prefix_x, keep_theta=plan_log is not None)
+    plan.record(plan_log)
     nnz = int(plan.kv.nnz_d.item())               # the one host read of the chunk
     return fused_chunk_execute(plan, q_chunk, index, nnz, sm_scale=sm_scale,
                                fa3_page_size=fa3_page_size, out=out, timing=timing,
@@ -175,14 +189,14 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
 
 def fused_decode_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor, *,
                            temperature: float, beta: float, target_tokens: int, sm_scale: float,
-                           iters: int = 16, num_splits: int = 64,
+                           iters: int = 16, num_splits: int = 64, csr_out=None,
                            **unused) -> PagedSparseAttentionResult:
     """One decode query over the packed prompt, selection against the full cluster
     sizes (fused_prefill.py:625-718).  The generated suffix is merged by the caller."""
     from .fused_decode import decode_prompt_only
     return decode_prompt_only(q_chunk, query_state.vectors[0], index, temperature=temperature,
                               beta=beta, target_tokens=target_tokens, sm_scale=sm_scale,
-                              iters=iters, num_splits=num_splits)
+                              iters=iters, num_splits=num_splits, csr_out=csr_out)
 
 
 def merge_paged_attention_results(left: PagedSparseAttentionResult,

@@ -53,6 +53,8 @@ class SembloAttention:
         self.index: ProductPostingIndex | None = None
         self.arena: DecodeArena | None = None
         self.target_tokens = 0
+        # test hook: a list here receives every sparse chunk's selection (ChunkPlan.record)
+        self.plan_log: list | None = None
         register_layer(self.layer_name, self)
 
     # -- routing (S0) ---------------------------------------------------------
@@ -183,7 +185,9 @@ class SembloAttention:
                 pl = fused_chunk_plan(q[st:en], self._query_state(qp[st:en]), index, snapshot, st,
                                       en - 1, temperature=cfg.selection_temperature,
                                       beta=cfg.bucket_size_penalty, target_tokens=self.target_tokens,
-                                      iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x)
+                                      iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x,
+                                      keep_theta=self.plan_log is not None)
+                pl.record(self.plan_log)
                 nnz_host[i:i + 1].copy_(pl.kv.nnz_d, non_blocking=True)
                 ev = torch.cuda.Event()
                 ev.record(side)

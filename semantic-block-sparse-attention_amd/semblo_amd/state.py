@@ -107,8 +107,8 @@ class ProductPostingIndex:
               flat_unit_tokens: int = 2048, flat_min_clusters_log2: int = 7, page_align: int = 16,
               descriptor_weight=None, descriptor_bias=None, descriptor_activation: str = "softplus",
               layer_idx: int | None = None, router_pass: bool = False,
-              fit_iters: int | None = None, num_clusters: int | None = None
-              ) -> "ProductPostingIndex":
+              fit_iters: int | None = None, num_clusters: int | None = None,
+              fit_trace: list | None = None) -> "ProductPostingIndex":
         """Fit the flat codebook and the posting lists (state.py:477-542 contract).
 
         ``product_keys`` [L, Hkv, I] bf16 are the key router's output (or, with
@@ -117,6 +117,12 @@ class ProductPostingIndex:
         ``quantizer`` and ``kmeans_init`` are accepted for signature parity;
         the flat path uses ``SEMBLO_FLAT_FIT_ITERS`` (default 8) iterations and
         32 sample points per centroid, as the reference does.
+
+        ``fit_trace``, if given, receives one dict per KV head with the fit's
+        intermediate states (the key space, the sample rows, and per iteration
+        the centroids it starts from, its assignment, sums and counts; then the
+        final centroids and assignment of every key), for parity checks of each
+        k-means step.  The iterations then run one call at a time.
         """
         if product_keys.ndim != 3:
             raise ValueError("product_keys must have shape [L,Hkv,I]")
@@ -188,9 +194,21 @@ class ProductPostingIndex:
             host.uploaded.record()
             return both[:fit_n], both[fit_n:]
 
+        steps: dict = {}
+
         def iterate(start, sample_idx):
             # k-means steps start.. with no restart rows, in one call; an iteration
             # that left a cluster empty is found afterwards from counts_hist and redone
+            if fit_trace is not None:
+                for i in range(start, iters):
+                    entry = cent_bf.clone()
+                    _lib.call("sbsa_kmeans_iterate", _lib.ptr(space_bf), _lib.ptr(space_f32),
+                              index_dim, _lib.ptr(sample_idx), fit_n, c, index_dim,
+                              _lib.ptr(assign_s), _lib.ptr(sums_hist), _lib.ptr(counts_hist),
+                              _lib.ptr(no_restart), _lib.ptr(cent_f32), _lib.ptr(cent_bf), i,
+                              i + 1, s)
+                    steps[i] = (entry, assign_s.clone())
+                return
             if start < iters:
                 _lib.call("sbsa_kmeans_iterate", _lib.ptr(space_bf), _lib.ptr(space_f32), index_dim,
                           _lib.ptr(sample_idx), fit_n, c, index_dim, _lib.ptr(assign_s),
@@ -236,6 +254,16 @@ class ProductPostingIndex:
                       _lib.ptr(inverse[h]), _lib.ptr(totals[h:h + 1]), _lib.ptr(ws), ws_bytes, s)
             _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
                       c, index_dim, None, _lib.ptr(codebooks[h]), s)
+            if fit_trace is not None:
+                fit_trace.append(dict(
+                    space_f32=space_f32.cpu(), space_bf16=space_bf.cpu(),
+                    sample=sample_idx.cpu().long(),
+                    entry_centroids=[steps[i][0].cpu() for i in range(iters)],
+                    assign=[steps[i][1].cpu().long() for i in range(iters)],
+                    sums=sums_hist[:iters].cpu(), counts=counts_hist[:iters].cpu(),
+                    final_centroids_f32=cent_f32.cpu(), final_centroids=cent_bf.cpu(),
+                    final_assign=assign_all.cpu().long()))
+                steps.clear()
             if h + 1 < hkv:
                 # the next head's draws, on the host while the GPU lays this head out
                 draws = draw_sample_and_init()

@@ -383,4 +383,4 @@ class TokenOuterPrefillSession:
                               temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
                               target_tokens=self.target, sm_scale=layer.scaling, iters=cfg.iters,
                               dense_prefix_x=cfg.dense_prefix_x, out=out, timing=timing,
-                              window_kv=(kk, vv))
+                              window_kv=(kk, vv), plan_log=layer.plan_log)

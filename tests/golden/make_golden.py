@@ -13,6 +13,9 @@ the vectors are kept.
                 settings (flat unit 2048, whole routing, 8 fit iterations,
                 page alignment 16).  The keys are regenerated from the seed by
                 tests/golden/synth.py; a checksum of them is stored.
+  router_*.pt   trivial_router_vectors (trivial_router.py:48-75) through its
+                torch path off the GPU (:55-61), on seeded bf16 queries with
+                rows of tiny, huge, zero and single-spike norms mixed in.
   select_*.pt   theta_select_bitmask_flat (fused_select.py:806-919) with the
                 torch-form scores (SEMBLO_FLAT_TORCH_SCORES=1, fused_select.py:
                 865-910) and the RESIDENT _streaming_select_kernel
@@ -126,6 +129,38 @@ def make_select(ref_root: str) -> None:
         print(name, "selected per query", counts.float().mean().item())
 
 
+ROUTER_CASES = [
+    # name, Q, Hq, D, factors, seed
+    ("router_q48_h4_d256", 48, 4, 256, 1, 31),
+    ("router_q32_h8_d128_f2", 32, 8, 128, 2, 32),
+    # tiny halves: the intermediate bf16 rounding shows in the output
+    ("router_q256_h4_d16_f2", 256, 4, 16, 2, 33),
+]
+
+
+def router_inputs(q: int, hq: int, d: int, seed: int) -> torch.Tensor:
+    """Seeded bf16 queries [Q, Hq, D]: Gaussian rows, then every 5th row scaled by
+    1e-3, every 7th by 1e3, row 3 zero and row 4 a single spike."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(q, hq, d, generator=gen)
+    x[::5] *= 1e-3
+    x[::7] *= 1e3
+    x[3] = 0.0
+    x[4] = 0.0
+    x[4, :, 7] = 5.0
+    return x.to(torch.bfloat16)
+
+
+def make_router(ref_root: str) -> None:
+    from semblo.vllm_plugin.trivial_router import trivial_router_vectors
+    for name, q, hq, d, factors, seed in ROUTER_CASES:
+        x = router_inputs(q, hq, d, seed)
+        out = trivial_router_vectors(x, factors)          # CPU tensor: the torch path
+        torch.save(dict(x=x, factors=torch.tensor(factors), out=out.contiguous()),
+                   HERE / f"{name}.pt")
+        print(name, tuple(out.shape))
+
+
 if __name__ == "__main__":
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     sys.path.insert(0, ref)
@@ -134,3 +169,5 @@ if __name__ == "__main__":
         make_kmeans(ref)
     if which in ("all", "select"):
         make_select(ref)
+    if which in ("all", "router"):
+        make_router(ref)

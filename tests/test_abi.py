@@ -78,3 +78,30 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert lib.sbsa_prefill_attend(p, 4096, 256, 128, 16, 4, 256, p, 1024, p, p, 1024, 256, p, p,
                                    64, p, p, p, p, p, p, p, 4096, 256, p, 512, 1024, 0.0625, 0,
                                    None) == 1
+
+
+def test_attend_refuses_windows_past_the_32bit_buffer_range():
+    """A window whose rows span 4 GiB or more (here a fused-QKV row stride of 12,288 and
+    200,000 positions) cannot be addressed by the tile loads' buffer resources: the entry
+    point refuses it (SBSA_ERR_UNSUPPORTED) instead of reading zeros past the wrap."""
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    lib = _lib.load()
+    p = 256
+    args = [p, 4096, 256, 128, 16, 4, 256, None, 0, p, p, 12288, 256, None, None, 32, None,
+            None, p, p, None, None, p, 4096, 256, None, 200000, 0, 0.0625, 0, None]
+    assert lib.sbsa_prefill_attend(*args) == 2
+
+
+def test_combine_refuses_rows_that_are_not_16_byte_aligned():
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    lib = _lib.load()
+    p = 256
+    # G * D = 1024: 16-byte row pieces; an output row stride of 4 elements is refused
+    assert lib.sbsa_prefill_combine(p, p, p, p, p, p, p, 4096, 256, p, p, 4, 256, None,
+                                    8, 16, 4, 256, 128, None) == 1
+    assert lib.sbsa_prefill_combine(p, p, p, p, p, p, p, 4100, 256, p, p, 4096, 256, None,
+                                    8, 16, 4, 256, 128, None) == 1

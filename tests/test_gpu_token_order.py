@@ -19,7 +19,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from gpu_util import assert_close_bf16, attention_reference, cluster_position_mask, oracle_select
+from gpu_util import (assert_close_bf16, attention_reference, check_recorded_chunk,
+                      cluster_position_mask, oracle_select)
 from oracle import reference_cpu as ref
 
 pytestmark = pytest.mark.gpu
@@ -168,6 +169,7 @@ def _run_session(cfg, k_override=None):
     rc = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=chunk,
                              codebook_seed=cfg["seed"], layer_idx=0)
     layer = SembloAttention(rc, layer_name=f"test.token_order.{cfg['seed']}")
+    layer.plan_log = []
     inp = mixture_layer(tokens, hq, hkv, d, mixtures=32, seg=(32, 256), seed=cfg["seed"])
     if k_override is not None:
         k_override(inp)
@@ -234,7 +236,8 @@ def test_token_order_session_store_and_attention(cfg):
     # attention, slice by slice
     target = session.target
     sm = d ** -0.5
-    bad_total = 0
+    recs = {r["chunk_start"]: r for r in layer.plan_log}
+    near_ties = 0
     for start in range(0, tokens, cfg["chunk"]):
         stop = min(tokens, start + cfg["chunk"])
         p = torch.arange(start, stop)
@@ -243,23 +246,14 @@ def test_token_order_session_store_and_attention(cfg):
             want = attention_reference(inp.q[start:stop], keys, inp.k, inp.v, sm)
             assert_close_bf16(out[start:stop], want, f"dense slice {start}")
             continue
-        sizes = before[start]
-        vec = ref.trivial_router_vectors(inp.q[start:stop], 1)
-        sel = oracle_select(vec, index.codebooks.cpu(), sizes[None], temperature=0.1, beta=0.25,
-                            target=target)["sel"]
-        pos = cluster_position_mask(posting, index.bucket_indptr.cpu(), sizes, tokens)
-        keys = torch.einsum("qhc,hcl->qhl", sel.double(), pos.double()) > 0
-        keys |= ((torch.arange(tokens)[None, :] >= start)
-                 & (torch.arange(tokens)[None, :] <= p[:, None]))[:, None, :]
-        want = attention_reference(inp.q[start:stop], keys, inp.k, inp.v, sm)
-        g = out[start:stop].double()
-        err = (g - want).abs() - (2e-2 + 1e-2 * want.abs())
-        bad_q = (err > 0).flatten(1).any(-1)
-        bad_total += int(bad_q.sum())
-        # near-tie selection differences move a handful of rows
-        assert int(bad_q.sum()) <= 2, f"slice {start}: {int(bad_q.sum())} queries off"
+        rec = recs[start]
+        assert torch.equal(rec["causal_sizes"].cpu(), before[start])
+        rep = check_recorded_chunk(rec, inp.q, inp.q, inp.k, inp.v, index, out, target=target,
+                                   tag="token order")
+        near_ties += rep["near_ties"]
     print(f"{cfg}: fit at {fit_at}, {len(ids_by_slice)} appended slices, {moved} near-tie ids, "
-          f"{session.repacks} repacks ({session.repacks_with_slice} counting the slice), {bad_total} queries beyond tolerance (near-tie selections)")
+          f"{session.repacks} repacks ({session.repacks_with_slice} counting the slice), {near_ties} near-tie selection "
+          f"differences against the oracle")
     assert layer.arena is not None and layer.arena.prompt_length == tokens
 
 

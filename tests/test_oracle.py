@@ -99,6 +99,26 @@ def test_router_closed_form():
     assert torch.allclose(ref.trivial_router_vectors(v, 1).float(), v.float(), atol=2 ** -8)
 
 
+@pytest.mark.parametrize("name", sorted(p.name for p in GOLDEN.glob("router_*.pt")))
+def test_router_matches_the_reference_golden(name):
+    """S0 bit for bit against vectors written by the reference's own router
+    (trivial_router.py:55-61, the torch path), and the fixtures are strong
+    enough that dropping the intermediate bf16 rounding or the eps fails."""
+    g = torch.load(GOLDEN / name, weights_only=True)
+    x, f = g["x"], int(g["factors"])
+    assert torch.equal(ref.trivial_router_vectors(x, f), g["out"])
+    q, h, d = x.shape
+    halves = x.float().view(q, h, f, d // f)
+    unit = halves / halves.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    no_eps = halves / halves.norm(dim=-1, keepdim=True)
+    no_eps = no_eps.to(x.dtype).float()
+    no_eps = (no_eps / no_eps.norm(dim=-1, keepdim=True)).to(x.dtype).view(q, h, d)
+    assert not torch.equal(no_eps, g["out"])           # the zero rows turn to NaN
+    if name.endswith("_d16_f2.pt"):
+        no_round = (unit / unit.norm(dim=-1, keepdim=True).clamp_min(1e-12)).to(x.dtype)
+        assert not torch.equal(no_round.view(q, h, d), g["out"])
+
+
 def test_cluster_count_rule():
     assert ref.num_flat_clusters(131072) == 128
     assert ref.num_flat_clusters(524288) == 256
