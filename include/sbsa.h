@@ -214,7 +214,8 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
  * table maps logical blocks prompt_len/suffix_block through
  * (prompt_len + 16*max_tiles - 1)/suffix_block.  num_splits + suffix_splits
  * <= 512.  No host reads, no allocation: capturable in a HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
- * then rcount [Hkv] and rtokens [Hkv]. */
+ * then rcount [Hkv] and rtokens [Hkv]; of each head's C entries only the first
+ * rcount[h] are written by the step (the rest keep earlier contents). */
 size_t sbsa_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int num_clusters, int dim,
                                    int num_splits, int suffix_splits);
 int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
@@ -227,6 +228,30 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
                      void* workspace, size_t workspace_bytes, void* out, int64_t out_sh,
                      float* out_lse, int32_t* csr_out, hipStream_t stream);
+
+/* The decode step with no allocation and no workspace argument.  This entry point
+ * has no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as sbsa_decode_step minus the
+ * workspace: the step's scratch (the selection's CSR and the splits' partials) is
+ * a static device array of the library, sbsa_decode_scratch_bytes() bytes per GPU,
+ * held until the process ends; shapes whose sbsa_decode_workspace_bytes exceeds it
+ * return SBSA_ERR_CAPACITY.  Its address is looked up once per device, on the
+ * first call with that device current (make that call before a capture).  Every
+ * call on a GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, or two processes' threads into one library) race. */
+size_t sbsa_decode_scratch_bytes(void);
+int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
+                             int router_pass, const void* k_new, const void* v_new, int64_t kn_sh,
+                             const int32_t* pos, const void* codebooks, const int32_t* sizes,
+                             const int32_t* indptr, const void* packed, int64_t packed_len,
+                             void* suffix_kv, int64_t suffix_nblk, int suffix_block,
+                             const int32_t* table, int64_t prompt_len, int max_tiles,
+                             int num_q_heads, int num_kv_heads, int num_clusters, int dim,
+                             float inv_temperature, float beta, float target_tokens, int iters,
+                             int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
+                             void* out, int64_t out_sh, float* out_lse, int32_t* csr_out,
+                             hipStream_t stream);
 
 /* ---- S10: token-order streamed prefill (the store behind the fixed clusters) -----
  * Nearest cluster of each new key: replaces _nearest_cluster

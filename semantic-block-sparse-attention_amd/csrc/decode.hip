@@ -25,6 +25,8 @@
 //   2. merge: one block per (query head, 64 dimensions) folds the splits.
 #include "sbsa_common.h"
 
+#include <mutex>
+
 namespace {
 
 struct DecodeArgs {
@@ -663,7 +665,13 @@ size_t sbsa_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int num_cl
          2 * (size_t)num_q_heads * s * 4;
 }
 
-int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
+}  // extern "C"
+
+namespace {
+
+// The step's body, shared by sbsa_decode_step (workspace from the caller) and
+// sbsa_decode_step_noalloc (the library's static scratch array).
+int decode_step_impl(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
                      int router_pass, const void* k_new, const void* v_new, int64_t kn_sh,
                      const int32_t* pos, const void* codebooks, const int32_t* sizes,
                      const int32_t* indptr, const void* packed, int64_t packed_len,
@@ -750,6 +758,83 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   }
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
+}
+
+// Scratch of the entry point that allocates nothing: one array per GPU, held
+// until the process ends.  Host code never passes `scratch` itself to a kernel
+// (in host code the name is a stand-in, not a device address): each device's
+// address is looked up once with hipGetSymbolAddress, with that device
+// current, and kept in scratch_ptr.
+constexpr size_t DECODE_SCRATCH_BYTES = (size_t)8 << 20;
+__device__ __align__(256) unsigned char scratch[DECODE_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[MAX_DEVICES] = {};
+
+// This device's scratch address, looked up on its first use (nullptr on failure).
+void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    scratch_ptr[dev] = p;
+  }
+  return scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
+                     int router_pass, const void* k_new, const void* v_new, int64_t kn_sh,
+                     const int32_t* pos, const void* codebooks, const int32_t* sizes,
+                     const int32_t* indptr, const void* packed, int64_t packed_len,
+                     void* suffix_kv, int64_t suffix_nblk, int suffix_block, const int32_t* table,
+                     int64_t prompt_len, int max_tiles, int num_q_heads, int num_kv_heads,
+                     int num_clusters, int dim, float inv_temperature, float beta,
+                     float target_tokens, int iters, int sink_tokens, float sm_scale,
+                     int num_splits, int suffix_splits, void* workspace, size_t workspace_bytes,
+                     void* out, int64_t out_sh, float* out_lse, int32_t* csr_out,
+                     hipStream_t stream) {
+  return decode_step_impl(q_post, q_sh, q_pre, qp_sh, router_pass, k_new, v_new, kn_sh, pos,
+                          codebooks, sizes, indptr, packed, packed_len, suffix_kv, suffix_nblk,
+                          suffix_block, table, prompt_len, max_tiles, num_q_heads, num_kv_heads,
+                          num_clusters, dim, inv_temperature, beta, target_tokens, iters,
+                          sink_tokens, sm_scale, num_splits, suffix_splits, workspace,
+                          workspace_bytes, out, out_sh, out_lse, csr_out, stream);
+}
+
+size_t sbsa_decode_scratch_bytes(void) { return DECODE_SCRATCH_BYTES; }
+
+int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre, int64_t qp_sh,
+                             int router_pass, const void* k_new, const void* v_new, int64_t kn_sh,
+                             const int32_t* pos, const void* codebooks, const int32_t* sizes,
+                             const int32_t* indptr, const void* packed, int64_t packed_len,
+                             void* suffix_kv, int64_t suffix_nblk, int suffix_block,
+                             const int32_t* table, int64_t prompt_len, int max_tiles,
+                             int num_q_heads, int num_kv_heads, int num_clusters, int dim,
+                             float inv_temperature, float beta, float target_tokens, int iters,
+                             int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
+                             void* out, int64_t out_sh, float* out_lse, int32_t* csr_out,
+                             hipStream_t stream) {
+  if (num_splits < 1 || suffix_splits < 1 || num_q_heads < 1 || num_kv_heads < 1 || dim < 1 ||
+      num_clusters < 1)
+    return SBSA_ERR_ARG;
+  const size_t need = sbsa_decode_workspace_bytes(num_q_heads, num_kv_heads, num_clusters, dim,
+                                                  num_splits, suffix_splits);
+  if (need > DECODE_SCRATCH_BYTES) return SBSA_ERR_CAPACITY;
+  void* ws = device_scratch();
+  if (!ws) return SBSA_ERR_LAUNCH;
+  return decode_step_impl(q_post, q_sh, q_pre, qp_sh, router_pass, k_new, v_new, kn_sh, pos,
+                          codebooks, sizes, indptr, packed, packed_len, suffix_kv, suffix_nblk,
+                          suffix_block, table, prompt_len, max_tiles, num_q_heads, num_kv_heads,
+                          num_clusters, dim, inv_temperature, beta, target_tokens, iters,
+                          sink_tokens, sm_scale, num_splits, suffix_splits, ws, need, out,
+                          out_sh, out_lse, csr_out, stream);
 }
 
 }  // extern "C"

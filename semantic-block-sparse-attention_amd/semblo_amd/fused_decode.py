@@ -48,17 +48,20 @@ def fused_decode_step(layer, arena, *, q_post: torch.Tensor, q_pre: torch.Tensor
                       output: torch.Tensor, temperature: float, beta: float, target_tokens: int,
                       sm_scale: float, num_splits: int, iters: int = 16,
                       suffix_splits: int | None = None, out_lse: torch.Tensor | None = None,
-                      csr_out: torch.Tensor | None = None) -> None:
+                      csr_out: torch.Tensor | None = None, no_alloc: bool = False) -> None:
     """The whole decode step of one layer into ``output`` [1, Hq*D] (fused_decode.py:393-521).
 
     ``positions`` [1] is the token's position as a device tensor; the arena
     (arena.DecodeArena) holds the index, the packed K/V and the suffix store.
+    ``no_alloc``: run sbsa_decode_step_noalloc, whose scratch is the library's
+    static per-GPU array (no workspace tensor is made); steps on one GPU must not
+    overlap.
     """
     hq, hkv, d = int(layer.num_heads), int(layer.num_kv_heads), int(layer.head_dim)
     c = int(arena.num_clusters)
     ss = int(suffix_splits or arena.suffix_splits)
-    ws = _workspace(arena, hq=hq, hkv=hkv, d=d, c=c, splits=int(num_splits), suffix_splits=ss,
-                    device=q_post.device)
+    ws = None if no_alloc else _workspace(arena, hq=hq, hkv=hkv, d=d, c=c, splits=int(num_splits),
+                                          suffix_splits=ss, device=q_post.device)
     q = q_post.reshape(hq, d)
     qp = q_pre.reshape(hq, d)
     if q.stride(-1) != 1 or qp.stride(-1) != 1:
@@ -71,15 +74,18 @@ def fused_decode_step(layer, arena, *, q_post: torch.Tensor, q_pre: torch.Tensor
         kk = k_post.reshape(hkv, d)
         vv = v_states.reshape(hkv, d)
     out = output.reshape(hq, d)
-    _lib.call("sbsa_decode_step", _lib.ptr(q), q.stride(0), _lib.ptr(qp), qp.stride(0), 1,
-              _lib.ptr(kk), _lib.ptr(vv), kk.stride(0) if kk is not None else 0, _lib.ptr(pos),
-              _lib.ptr(arena.codebooks), _lib.ptr(arena.sizes), _lib.ptr(arena.indptr),
-              _lib.ptr(arena.packed_kv), arena.packed_kv.shape[1], _lib.ptr(arena.suffix_kv),
-              arena.suffix_kv.shape[1], arena.suffix_block, _lib.ptr(arena.suffix_table),
-              arena.prompt_length, arena.max_tiles, hq, hkv, c, d, 1.0 / float(temperature),
-              float(beta), float(target_tokens), int(iters), 0, float(sm_scale), int(num_splits),
-              ss, _lib.ptr(ws.buffer), ws.nbytes, _lib.ptr(out), out.stride(0),
-              _lib.ptr(out_lse), _lib.ptr(csr_out), _lib.stream(q.device))
+    head = (_lib.ptr(q), q.stride(0), _lib.ptr(qp), qp.stride(0), 1,
+            _lib.ptr(kk), _lib.ptr(vv), kk.stride(0) if kk is not None else 0, _lib.ptr(pos),
+            _lib.ptr(arena.codebooks), _lib.ptr(arena.sizes), _lib.ptr(arena.indptr),
+            _lib.ptr(arena.packed_kv), arena.packed_kv.shape[1], _lib.ptr(arena.suffix_kv),
+            arena.suffix_kv.shape[1], arena.suffix_block, _lib.ptr(arena.suffix_table),
+            arena.prompt_length, arena.max_tiles, hq, hkv, c, d, 1.0 / float(temperature),
+            float(beta), float(target_tokens), int(iters), 0, float(sm_scale), int(num_splits), ss)
+    tail = (_lib.ptr(out), out.stride(0), _lib.ptr(out_lse), _lib.ptr(csr_out), _lib.stream(q.device))
+    if no_alloc:
+        _lib.call("sbsa_decode_step_noalloc", *head, *tail)
+    else:
+        _lib.call("sbsa_decode_step", *head, _lib.ptr(ws.buffer), ws.nbytes, *tail)
 
 
 class _PromptOnly:

@@ -105,3 +105,20 @@ def test_combine_refuses_rows_that_are_not_16_byte_aligned():
                                     8, 16, 4, 256, 128, None) == 1
     assert lib.sbsa_prefill_combine(p, p, p, p, p, p, p, 4100, 256, p, p, 4096, 256, None,
                                     8, 16, 4, 256, 128, None) == 1
+
+
+def test_decode_without_allocation_refuses_shapes_past_its_scratch():
+    """sbsa_decode_step_noalloc returns SBSA_ERR_CAPACITY (4) before any GPU call when the
+    step's scratch would pass the library's static array."""
+    from semblo_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsbsa.so is not built here")
+    lib = _lib.load()
+    p = 256
+    cap = lib.sbsa_decode_scratch_bytes()
+    assert cap == 8 << 20
+    # 64 query heads x 500 splits x 256 dims of fp32 partials: far past 8 MiB
+    assert _lib.query("sbsa_decode_workspace_bytes", 64, 8, 1024, 256, 492, 8) > cap
+    assert lib.sbsa_decode_step_noalloc(p, 256, p, 256, 1, None, None, 0, p, p, p, p, p, 1000, p,
+                                        4, 256, p, 1000, 4, 64, 8, 1024, 256, 10.0, 0.25, 100.0,
+                                        16, 0, 0.0625, 492, 8, p, 256, None, None, None) == 4
