@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
   __shared__ int s_items[2];
   __shared__ int s_queue[16];
-  __shared__ int s_qslots[2][QPI];
+  __shared__ int s_qslots[2][QPI < 64 ? 64 : QPI];   // a whole wave's lanes per row (the fetch writes 64)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -948,7 +948,14 @@ int launch_combine(const int32_t* qmask, const int32_t* nvis, const int32_t* rev
 
 #define SBSA_DISPATCH_DG(D_, G_, FN, ...)                            \
   do {                                                               \
+    if (D_ == 128 && G_ == 1) return FN<128, 1>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 2) return FN<128, 2>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 4) return FN<128, 4>(__VA_ARGS__);        \
+    if (D_ == 128 && G_ == 8) return FN<128, 8>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 1) return FN<256, 1>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 2) return FN<256, 2>(__VA_ARGS__);        \
     if (D_ == 256 && G_ == 4) return FN<256, 4>(__VA_ARGS__);        \
+    if (D_ == 256 && G_ == 8) return FN<256, 8>(__VA_ARGS__);        \
     return SBSA_ERR_UNSUPPORTED;                                     \
   } while (0)
 
