@@ -690,6 +690,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           const int c = (4 * dt + 2 * p + g) ^ (l32 & (S::CH - 1));
           *reinterpret_cast<u32x4_t*>(stage + l32 * S::ROW_BYTES + 16 * c) = w;
         }
+      // the wave's lanes hand their rows to each other through the staging
+      // slice (in order on the GPU, where a wave's LDS operations run in issue
+      // order; the barrier keeps the compiler from moving them)
+      __builtin_amdgcn_wave_barrier();
       // read back whole rows (instruction m covers rows ROWS_PER_INST m ..),
       // reads first, then the stores, so no store waits on a single read
       constexpr int NR = 32 / S::ROWS_PER_INST;
