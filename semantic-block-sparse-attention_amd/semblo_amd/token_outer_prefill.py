@@ -29,6 +29,10 @@ does (token_outer_prefill.py:155-159).
 Host reads: one per appended slice (the overflow flags, the reference's
 ``bool((sizes + counts > reserve).any())``), and the cluster sizes at the
 fit and at a repack, from which the reserved layout is computed on the host.
+They arrive by an asynchronous copy into pinned memory.  A sparse slice reads
+no row of its own slice from the store, so its attention is enqueued between
+the assignment and that read: the GPU runs it while the host waits for the
+flags and lays out any repack, which then follows the attention on the stream.
 """
 from __future__ import annotations
 
@@ -175,6 +179,7 @@ class TokenOuterPrefillSession:
         self.repacks_with_slice = 0                 # repacks whose layout counts the slice's keys
         self.next_start = 0
         self._spare: torch.Tensor | None = None     # the other buffer of the store, after a repack
+        self._host: torch.Tensor | None = None      # pinned: the append's flags, counts and sizes
         self.verbose = os.environ.get("SEMBLO_VERBOSE", "0") == "1"
         layer.target_tokens = self.target
 
@@ -205,9 +210,20 @@ class TokenOuterPrefillSession:
             self._count_dense(timing, start, n, hq, d)
             dense_causal_attention(q, self.stage_k[:stop], self.stage_v[:stop], sm_scale=layer.scaling,
                                    chunk_start=start, out=out, timing=timing)
-        else:
-            self._append(kp, kk, vv, start, stop, store_timing)
+        elif start <= self.cap:
+            # a dense-prefix slice reads its own keys back from the store: append first
+            self._append_commit(self._append_assign(kp, start, stop, store_timing), kk, vv, store_timing)
             self._attend(q, qp, kk, vv, start, stop, out, timing)
+        else:
+            # A sparse slice reads only rows of earlier positions (the counts before it);
+            # its own keys come through the exact window.  Its attention is therefore
+            # enqueued before the append's host read, and the GPU runs it while the host
+            # waits for the flags and lays out any repack.
+            pending = self._append_assign(kp, start, stop, store_timing)
+            self.snapshot.sizes.copy_(self.index.bucket_sizes)
+            self.snapshot.chunk_start = start
+            self._attend(q, qp, kk, vv, start, stop, out, timing)
+            self._append_commit(pending, kk, vv, store_timing)
         self.next_start = stop
         return out
 
@@ -282,20 +298,40 @@ class TokenOuterPrefillSession:
         self.stage_k = self.stage_v = self.stage_kpre = None
 
     # -- append ---------------------------------------------------------------------------
-    def _append(self, kp, kk, vv, start, stop, store_timing=None) -> None:
+    def _append_assign(self, kp, start, stop, store_timing=None):
+        """Enqueue the slice's assignment and the copy of what the host decides on:
+        overflow flags, the slice's counts and the sizes so far, into pinned memory."""
         index = self.index
-        hkv, d = kk.shape[1], kk.shape[2]
+        hkv = kp.shape[1]
         c = index.num_buckets
-        n = stop - start
-        s = _lib.stream(kk.device)
+        s = _lib.stream(kp.device)
         if store_timing is not None:
             store_timing.begin(s)
         ids = nearest_cluster(kp, index.codebooks, router_pass=True)
         rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
         if store_timing is not None:
             store_timing.end(s)
-        # the one host read per slice: flags, the slice's counts and the sizes so far
-        host = torch.cat([flags, counts.flatten(), index.bucket_sizes.flatten()]).cpu()
+        words = hkv + 2 * hkv * c
+        if self._host is None or self._host.numel() != words:
+            self._host = torch.empty(words, dtype=torch.int32, pin_memory=True)
+        self._host.copy_(torch.cat([flags, counts.flatten(), index.bucket_sizes.flatten()]),
+                         non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(kp.device))
+        return dict(ids=ids, rows=rows, counts=counts, ready=ready, start=int(start), stop=int(stop))
+
+    def _append_commit(self, pending, kk, vv, store_timing=None) -> None:
+        """The append's one host read per slice, any repack it decides, and the K/V
+        writes (token_outer_prefill.py:339-364)."""
+        index = self.index
+        hkv, d = kk.shape[1], kk.shape[2]
+        c = index.num_buckets
+        start, stop = pending["start"], pending["stop"]
+        n = stop - start
+        s = _lib.stream(kk.device)
+        ids, rows, counts = pending["ids"], pending["rows"], pending["counts"]
+        pending["ready"].synchronize()
+        host = self._host
         flags_h = host[:hkv]
         if bool((flags_h & 2).any()):
             raise RuntimeError("a key was assigned outside the cluster range")
