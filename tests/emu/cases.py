@@ -196,3 +196,19 @@ def _debug_dense(length: int, hq: int, hkv: int, d: int, cs: int, ce: int, seed:
     print("dims 96..127 got ", out[q0, 0, 96:128])
     print("dims 96..127 want", want[q0, 0, 96:128].float())
     print("bad dims of q0 h0:", torch.nonzero(bad[q0, 0]).flatten().tolist())
+
+
+def gpu_tests(*node_ids: str) -> None:
+    """GPU test functions (tests/test_gpu_*.py node ids) against the emulated library:
+    each module's device is set to the CPU before pytest collects it, so the tests
+    run unchanged, every kernel under the address sanitizer."""
+    import importlib
+    import pytest
+    for node in node_ids:
+        mod = importlib.import_module(Path(node.split("::")[0]).stem)
+        mod.DEV = "cpu"
+    rc = pytest.main([str(TESTS / n) for n in node_ids] +
+                     ["-m", "gpu", "-q", "-p", "no:cacheprovider", "-p", "no:randomly"])
+    if rc != 0:
+        raise SystemExit(f"emulated GPU tests failed: pytest exit {int(rc)}")
+    print(f"emulated GPU tests: {len(node_ids)} node ids passed")

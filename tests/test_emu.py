@@ -60,3 +60,11 @@ def test_emulated_sparse_chunk():
 
 def test_emulated_decode_steps():
     _run("decode_steps", 1024, 8, 2, 128, 5)
+
+
+def test_gpu_selection_and_append_tests_under_emulation():
+    """The selection tests and the token-order append tests, run unchanged on the
+    emulated kernels (each kernel's every memory access under the sanitizer)."""
+    _run("gpu_tests", "test_gpu_select.py",
+         "test_gpu_token_order.py::test_append_rows_bit_exact",
+         "test_gpu_token_order.py::test_append_rows_flags_an_id_out_of_range", timeout=900)
