@@ -175,6 +175,7 @@ class TokenOuterPrefillSession:
         self.index: ProductPostingIndex | None = None
         self.snapshot: TokenOuterSnapshot | None = None
         self.reserve: torch.Tensor | None = None
+        self._reserve_dev: torch.Tensor | None = None
         self.repacks = 0
         self.repacks_with_slice = 0                 # repacks whose layout counts the slice's keys
         self.next_start = 0
@@ -182,6 +183,14 @@ class TokenOuterPrefillSession:
         self._host: torch.Tensor | None = None      # pinned: the append's flags, counts and sizes
         self.verbose = os.environ.get("SEMBLO_VERBOSE", "0") == "1"
         layer.target_tokens = self.target
+
+    def _set_reserve(self, reserve: torch.Tensor, device) -> None:
+        """The reservation [Hkv, C] on the host (for the layout) and on the device (for
+        the overflow test), the latter by an asynchronous copy from pinned memory, so
+        that setting it never waits for the GPU."""
+        self.reserve = reserve
+        staged = reserve.to(torch.int32).pin_memory()
+        self._reserve_dev = staged.to(device, non_blocking=True)
 
     # -- per slice ------------------------------------------------------------------
     def slice(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
@@ -273,7 +282,7 @@ class TokenOuterPrefillSession:
         c = index.num_buckets
         width = self.tokens + c * align
         width += (-width) % PACK_ALIGN
-        self.reserve = reserved_layout(index.bucket_sizes, p, self.tokens, width, align)
+        self._set_reserve(reserved_layout(index.bucket_sizes, p, self.tokens, width, align), dev)
         indptr_h = torch.zeros(hkv, c + 1, dtype=torch.int32)
         indptr_h[:, 1:] = torch.cumsum(self.reserve, 1).to(torch.int32)
         indptr = indptr_h.to(dev)
@@ -308,7 +317,7 @@ class TokenOuterPrefillSession:
         if store_timing is not None:
             store_timing.begin(s)
         ids = nearest_cluster(kp, index.codebooks, router_pass=True)
-        rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
+        rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self._reserve_dev)
         if store_timing is not None:
             store_timing.end(s)
         words = hkv + 2 * hkv * c
@@ -379,9 +388,9 @@ class TokenOuterPrefillSession:
         packed = index.packed_kv
         hkv, width, d = packed.shape[2], packed.shape[1], packed.shape[3]
         c = index.num_buckets
-        new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32)
+        new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32, pin_memory=True)
         new_ip[:, 1:] = torch.cumsum(reserve, 1).to(torch.int32)
-        new_ip = new_ip.to(packed.device)
+        new_ip = new_ip.to(packed.device, non_blocking=True)
         if self._spare is None:
             self._spare = torch.zeros_like(packed)
         dst = self._spare
@@ -393,7 +402,7 @@ class TokenOuterPrefillSession:
                   _lib.stream(packed.device))
         index.packed_kv, self._spare = dst, packed
         index.bucket_indptr.copy_(new_ip)                             # same address as before
-        self.reserve = reserve
+        self._set_reserve(reserve, packed.device)
         index.extras["reserve"] = reserve
         self.repacks += 1
         if self.verbose:

@@ -77,7 +77,15 @@ def _host_cuda_surface() -> None:
         k.pop("pin_memory", None)
         return empty(*a, **k)
 
+    zeros = torch.zeros
+
+    def zeros_unpinned(*a, **k):
+        k.pop("pin_memory", None)
+        return zeros(*a, **k)
+
     torch.empty = empty_unpinned
+    torch.zeros = zeros_unpinned
+    torch.Tensor.pin_memory = lambda self, *a, **k: self
     torch.cuda.Event = _Event
     torch.cuda.Stream = _Stream
     torch.cuda.current_stream = lambda *a, **k: _Stream()
