@@ -62,12 +62,13 @@ def _check_index_invariants(idx, length):
         assert (seen == 1).all(), "every position in exactly one cluster"
 
 
-def _traced_builds(product, codebook_seed, **kw):
+def _traced_builds(product, codebook_seed, sink=0, **kw):
     """The GPU build with its fit trace, and the oracle's build with its steps."""
     trace = []
-    idx = _build_gpu(product, codebook_seed=codebook_seed, fit_trace=trace, **kw)
+    idx = _build_gpu(product, codebook_seed=codebook_seed, fit_trace=trace, sink_tokens=sink, **kw)
     steps = []
     want = ref.build_flat_index(product, codebook_seed=codebook_seed, fit_steps=steps,
+                               sink_tokens=sink,
                                **({"min_clusters_log2": kw["flat_min_clusters_log2"]}
                                   if "flat_min_clusters_log2" in kw else {}))
     return idx, trace, want, steps
@@ -79,11 +80,16 @@ def _check_trace(product, idx, trace, want, steps, tag):
     reps = []
     posting_gpu = idx.posting_positions.cpu()
     for h, (tr, st) in enumerate(zip(trace, steps)):
-        rep = check_fit_trace(product[:, h], tr, st["steps"], st["final_assign"],
+        sink = int(tr.get("sink", 0))
+        # with a sink the fit (and its trace) covers positions sink.. only
+        rep = check_fit_trace(product[sink:, h], tr, st["steps"], st["final_assign"],
                               st["final_centroids"], tag=f"{tag} head {h}")
         reps.append(rep)
         # the bucket layout of the GPU's assignment is the oracle's layout of it, bit for bit
-        a = tr["final_assign"]
+        a = tr["partition"]
+        if sink:
+            assert torch.equal(a[:sink], torch.zeros(sink, dtype=a.dtype))
+            assert torch.equal(a[sink:], tr["final_assign"] + 1)
         order = torch.argsort(a, stable=True)
         counts = torch.bincount(a, minlength=idx.num_buckets).to(torch.int32)
         length = a.numel()
@@ -106,8 +112,13 @@ def test_build_matches_the_reference_golden(name):
     length, hkv, d = int(g["length"]), int(g["hkv"]), int(g["d"])
     k_pre = golden_keys(length, hkv, d, int(g["seed"]), mixture=name.endswith("_mix.pt"))
     product = ref.routing_normalize_keys(k_pre)
-    idx, trace, want, steps = _traced_builds(product, int(g["codebook_seed"]),
+    sink = int(g["sink"]) if "sink" in g else 0
+    idx, trace, want, steps = _traced_builds(product, int(g["codebook_seed"]), sink=sink,
                                              flat_min_clusters_log2=int(g["min_log2"]))
+    if sink:
+        # cluster 0 holds positions 0..S-1 and nothing else; its descriptor is zero
+        assert (idx.bucket_sizes[:, 0].cpu() == sink).all()
+        assert torch.count_nonzero(idx.codebooks[:, :, 0].cpu()) == 0
     _check_index_invariants(idx, length)
     assert torch.equal(want["posting"], g["posting"])       # the oracle is the reference here
     reps = _check_trace(product, idx, trace, want, steps, name)
