@@ -241,6 +241,13 @@ class SembloAttention:
         if self.arena is None:
             raise RuntimeError("decode before any prefill: the layer has no index")
         cfg = self.runtime_config
+        # The suffix store holds `reserve` generated positions (the reference sizes it to the
+        # model's room for generated tokens, arena.py:50-63); a step past it would neither
+        # store nor read its token, so it is refused here, counted on the host.
+        if self.arena.steps >= self.arena.reserve:
+            raise RuntimeError(f"the decode suffix holds {self.arena.reserve} generated positions "
+                               f"(suffix_reserve); raise it to the generation length")
+        self.arena.steps += 1
         fused_decode_step(self, self.arena, q_post=q_post, q_pre=q_pre, positions=positions,
                           k_post=k_post, v_states=v, output=output,
                           temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
