@@ -198,73 +198,88 @@ __global__ __launch_bounds__(256) void kmeans_assign_kernel(
 }
 
 // Per-cluster fp32 sums of the member rows, in row order (deterministic).
-// One block per cluster takes the assignment in chunks of 4096 rows: each
-// wave compacts the members of its 1024 contiguous rows into its own list
-// (ballots, no block barrier), the four lists form the chunk's members in row
-// order, and each thread adds its dimensions of those rows in that order with
-// eight rows' loads in flight.
-constexpr int KU_CHUNK = 4096;
+// One block per cluster.  The work per launch is a few MB; what it costs is
+// dependent load round trips, so the kernel is shaped to need few of them.
+// The assignment is scanned in chunks of 8192 rows: each wave loads the
+// assignment (and the row map) of its 2048 contiguous rows in one go, 32
+// values a lane, counts its members with ballots, and after one block barrier
+// writes them at its offset of a block-wide member list, so the list holds the
+// cluster's rows in row order across chunks.  The list is summed only when the
+// next chunk could overflow it, or at the end -- for a typical cluster once --
+// each thread adding its dimensions of the listed rows in list order, the loads
+// of KU_BATCH rows issued before any of them is added.
+constexpr int KU_CHUNK = 8192;
+constexpr int KU_PER_LANE = KU_CHUNK / 4 / 64;   // 32 rows a lane per chunk
+constexpr int KU_LIST = 3 * KU_CHUNK / 2;        // member list capacity (48 KB)
+constexpr int KU_BATCH = 32;
 
+template <int NJ>  // dims threadIdx.x + 256*j for j < NJ
 __global__ __launch_bounds__(256) void kmeans_update_kernel(
     const float* __restrict__ x, int64_t ld_x, const int32_t* __restrict__ row_index, int64_t n,
     const int32_t* __restrict__ assign, int dim, float* __restrict__ sums,
     int32_t* __restrict__ counts) {
-  __shared__ int members[KU_CHUNK];        // source rows, wave w's at [w * 1024, ...)
+  __shared__ int members[KU_LIST];
   __shared__ int wave_cnt[4];
   const int c = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint64_t below = (1ull << lane) - 1;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims threadIdx.x + 256*j, dim <= 1024
-  int total = 0;
+  float acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = 0.f;
+  int total = 0;     // members summed so far
+  int listed = 0;    // members in the list, not yet summed
   for (int64_t base = 0; base < n; base += KU_CHUNK) {
     const int64_t seg = base + wave * (KU_CHUNK / 4);
-    int cnt_w = 0;
-#pragma unroll 4
-    for (int k = 0; k < KU_CHUNK / 4 / 64; ++k) {
+    int a[KU_PER_LANE], r[KU_PER_LANE];
+#pragma unroll
+    for (int k = 0; k < KU_PER_LANE; ++k) {
       const int64_t i = seg + k * 64 + lane;
-      const bool mine = i < n && assign[i] == c;
-      const uint64_t ball = __ballot(mine);
-      if (mine) members[wave * (KU_CHUNK / 4) + cnt_w + __popcll(ball & below)] =
-          row_index ? row_index[i] : (int)i;
-      cnt_w += __popcll(ball);
+      a[k] = i < n ? assign[i] : -1;
+      r[k] = i < n ? (row_index ? row_index[i] : (int)i) : 0;
     }
+    int cnt_w = 0;
+#pragma unroll
+    for (int k = 0; k < KU_PER_LANE; ++k) cnt_w += __popcll(__ballot(a[k] == c));
     if (lane == 0) wave_cnt[wave] = cnt_w;
     __syncthreads();
-    for (int w = 0; w < 4; ++w) {
-      const int* lst = members + w * (KU_CHUNK / 4);
-      const int cnt = wave_cnt[w];
-      int m = 0;
-      for (; m + 8 <= cnt; m += 8) {
-        float v[8][4];
+    int at = listed;
+    for (int w = 0; w < wave; ++w) at += wave_cnt[w];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int64_t src = lst[m + u];
+    for (int k = 0; k < KU_PER_LANE; ++k) {
+      const bool mine = a[k] == c;
+      const uint64_t ball = __ballot(mine);
+      if (mine) members[at + __popcll(ball & below)] = r[k];
+      at += __popcll(ball);
+    }
+    listed += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    __syncthreads();    // the list is complete; wave_cnt may be rewritten
+    if (listed > KU_LIST - KU_CHUNK || base + KU_CHUNK >= n) {
+      for (int m = 0; m < listed; m += KU_BATCH) {
+        float v[KU_BATCH][NJ];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+        for (int u = 0; u < KU_BATCH; ++u) {
+          const bool ok = m + u < listed;
+          const int64_t src = ok ? members[m + u] : 0;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
             const int d = threadIdx.x + 256 * j;
-            v[u][j] = d < dim ? x[src * ld_x + d] : 0.f;
+            v[u][j] = (ok && d < dim) ? x[src * ld_x + d] : 0.f;
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < KU_BATCH; ++u)
+          if (m + u < listed)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[j] += v[u][j];
+            for (int j = 0; j < NJ; ++j) acc[j] += v[u][j];
       }
-      for (; m < cnt; ++m) {
-        const int64_t src = lst[m];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = threadIdx.x + 256 * j;
-          if (d < dim) acc[j] += x[src * ld_x + d];
-        }
-      }
-      total += cnt;
+      total += listed;
+      listed = 0;
+      __syncthreads();  // the list is free for the next chunk
     }
-    __syncthreads();
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     int d = threadIdx.x + 256 * j;
     if (d < dim) sums[(int64_t)c * dim + d] = acc[j];
   }
@@ -665,8 +680,11 @@ int sbsa_kmeans_update(const float* x, int64_t ld_x, const int32_t* row_index, i
                        int32_t* counts, hipStream_t stream) {
   if (!x || !assign || !sums || !counts || n < 0 || num_clusters < 1) return SBSA_ERR_ARG;
   if (dim < 1 || dim > 1024) return SBSA_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kmeans_update_kernel, dim3(num_clusters), dim3(256), 0, stream, x, ld_x,
-                     row_index, n, assign, dim, sums, counts);
+  auto kernel = dim <= 256 ? kmeans_update_kernel<1>
+                : dim <= 512 ? kmeans_update_kernel<2>
+                : dim <= 768 ? kmeans_update_kernel<3> : kmeans_update_kernel<4>;
+  hipLaunchKernelGGL(kernel, dim3(num_clusters), dim3(256), 0, stream, x, ld_x, row_index, n,
+                     assign, dim, sums, counts);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }

@@ -214,3 +214,36 @@ def test_build_with_empty_clusters_matches_the_oracle():
     if all(r["origin_flips"] == 0 for r in reps):
         assert gpu_empties == empties
         assert torch.equal(idx.posting_positions.cpu(), want["posting"])
+
+
+@pytest.mark.parametrize("dim", [256, 320])
+def test_update_sums_each_cluster_in_row_order(dim):
+    """The centroid sums through the C-ABI on a skewed assignment: cluster 0 holds
+    most rows (more than the kernel lists before it sums), cluster 5 none, the row
+    count is ragged and the rows are read through a row map.  Each sum must equal the
+    sequential fp32 sum of its member rows in row order, bit for bit."""
+    import numpy as np
+    from semblo_amd import _lib
+    gen = torch.Generator().manual_seed(11)
+    rows, n, c = 12000, 9000 + 37, 64
+    x = torch.randn(rows, dim, generator=gen)
+    row_index = torch.randperm(rows, generator=gen)[:n].to(torch.int32)
+    assign = torch.randint(1, c, (n,), generator=gen, dtype=torch.int32)
+    assign[torch.rand(n, generator=gen) < 0.7] = 0
+    assign[assign == 5] = 6
+    xd, rd, ad = x.to(DEV), row_index.to(DEV), assign.to(DEV)
+    sums = torch.full((c, dim), float("nan"), device=DEV)
+    counts = torch.full((c,), -1, dtype=torch.int32, device=DEV)
+    _lib.call("sbsa_kmeans_update", _lib.ptr(xd), dim, _lib.ptr(rd), n, _lib.ptr(ad), c, dim,
+              _lib.ptr(sums), _lib.ptr(counts), _lib.stream(xd.device))
+    torch.cuda.synchronize()
+    xs = x.numpy()[row_index.long().numpy()]
+    a = assign.numpy()
+    want = np.zeros((c, dim), np.float32)
+    for cl in range(c):
+        m = xs[a == cl]
+        if len(m):
+            want[cl] = np.cumsum(m, axis=0, dtype=np.float32)[-1]    # sequential, row order
+    assert int((a == 0).sum()) > 4096 and int((a == 5).sum()) == 0
+    assert torch.equal(counts.cpu(), torch.bincount(assign.long(), minlength=c).to(torch.int32))
+    assert np.array_equal(sums.cpu().numpy(), want)
