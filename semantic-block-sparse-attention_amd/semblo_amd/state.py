@@ -35,6 +35,8 @@ from . import _lib
 from .config import check_sink_partition, fitted_sink_tokens, num_flat_clusters
 
 PACK_ALIGN = 256
+# restart draws of the k-means fit made ahead per KV head (the GPU applies them)
+RESTARTS_AHEAD = 2
 
 
 class _DrawBuffers:
@@ -43,9 +45,13 @@ class _DrawBuffers:
     and the sample and initial rows go to the device from pinned memory."""
 
     def __init__(self, length: int, fit_n: int, c: int):
+        self.sub = torch.empty(fit_n, dtype=torch.int64)        # a host-side restart's draw
+        # a head's draws: sample permutation, init rows, restart rows drawn ahead
         self.perm = torch.empty(length, dtype=torch.int64)
-        self.sub = torch.empty(fit_n, dtype=torch.int64)
-        self.pinned = torch.empty(fit_n + c, dtype=torch.int32, pin_memory=True)
+        self.init = torch.empty(fit_n, dtype=torch.int64)
+        self.restarts = torch.empty(RESTARTS_AHEAD, fit_n, dtype=torch.int64)
+        self.pinned = torch.empty(fit_n + (1 + RESTARTS_AHEAD) * c, dtype=torch.int32,
+                                  pin_memory=True)
         self.uploaded = None            # event after the last upload from `pinned`
         self.counts = None              # pinned [iterations, C] cluster counts
 
@@ -180,6 +186,7 @@ class ProductPostingIndex:
         sums_hist = torch.empty(n_it, cf, index_dim, dtype=torch.float32, device=dev)
         counts_hist = torch.empty(n_it, cf, dtype=torch.int32, device=dev)
         no_restart = torch.full((cf,), -1, dtype=torch.int32, device=dev)
+        restart_flags = torch.zeros(n_it + 1, dtype=torch.int32, device=dev)   # [0] stays 0
         assign_s = torch.empty(fit_n, dtype=torch.int32, device=dev)
         assign_all = torch.empty(length, dtype=torch.int32, device=dev)
         cap = length + c * (max(align, 1) - 1)
@@ -192,79 +199,76 @@ class ProductPostingIndex:
         desc_fit = torch.empty(2, cf, index_dim // 2, dtype=product_keys.dtype, device=dev) if sink else None
         # the rows the k-means sees: positions sink..
         fit_f32, fit_bf = space_f32[sink:], space_bf[sink:]
+        bits_bytes = _lib.query("sbsa_kmeans_member_bits_bytes", fit_n, cf)
+        member_bits = torch.empty(bits_bytes // 4, dtype=torch.int32, device=dev)
         ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
         host = _draw_buffers(n_fit, fit_n, cf)
         counts_host = host.counts_host(n_it, cf)
 
-        def draw_sample_and_init():
-            # fit_flat_codebook's first two draws (flat_index.py:237-262)
+        k_ahead = RESTARTS_AHEAD
+
+        def draw():
+            """fit_flat_codebook's first two draws (flat_index.py:237-262), then the
+            draws of the first k_ahead restarts (flat_index.py:277-283) made ahead: the
+            GPU applies the k-th at the k-th iteration that leaves a cluster empty.
+            Returns the generator's state before each restart draw, to take back the
+            draws no iteration needs, and uploads the draws from pinned memory."""
             torch.randperm(n_fit, generator=gen, out=host.perm)
-            torch.randperm(fit_n, generator=gen, out=host.sub)
+            torch.randperm(fit_n, generator=gen, out=host.init)
+            before = []
+            for k in range(k_ahead):
+                before.append(gen.get_state())
+                torch.randperm(fit_n, generator=gen, out=host.restarts[k])
             if host.uploaded is not None:
                 host.uploaded.synchronize()     # the previous upload has left `pinned`
+            total = fit_n + (1 + k_ahead) * cf
             host.pinned[:fit_n].copy_(host.perm[:fit_n])
-            host.pinned[fit_n:].copy_(host.sub[:cf])
-            both = torch.empty(fit_n + cf, dtype=torch.int32, device=dev)
-            both.copy_(host.pinned, non_blocking=True)
+            host.pinned[fit_n:fit_n + cf].copy_(host.init[:cf])
+            host.pinned[fit_n + cf:total].view(k_ahead, cf).copy_(host.restarts[:, :cf])
+            both = torch.empty(total, dtype=torch.int32, device=dev)
+            both.copy_(host.pinned[:total], non_blocking=True)
             host.uploaded = torch.cuda.Event()
             host.uploaded.record()
-            return both[:fit_n], both[fit_n:]
+            return both[:fit_n], both[fit_n:fit_n + cf], both[fit_n + cf:], before
 
         steps: dict = {}
 
-        def iterate(start, sample_idx):
-            # k-means steps start.. with no restart rows, in one call; an iteration
-            # that left a cluster empty is found afterwards from counts_hist and redone
-            if fit_trace is not None:
-                for i in range(start, iters):
-                    entry = cent_bf.clone()
-                    _lib.call("sbsa_kmeans_iterate", _lib.ptr(fit_bf), _lib.ptr(fit_f32),
-                              index_dim, _lib.ptr(sample_idx), fit_n, cf, index_dim,
-                              _lib.ptr(assign_s), _lib.ptr(sums_hist), _lib.ptr(counts_hist),
-                              _lib.ptr(no_restart), _lib.ptr(cent_f32), _lib.ptr(cent_bf), i,
-                              i + 1, s)
-                    steps[i] = (entry, assign_s.clone())
-                return
-            if start < iters:
+        def iterate(start, sample_idx, restart_rows=None):
+            # k-means steps start.. in one call.  With restart_rows the first k_ahead
+            # iterations that leave clusters empty restart them on the GPU; an iteration
+            # that left a cluster empty without a restart is found afterwards from
+            # counts_hist and redone
+            def call(i0, i1):
                 _lib.call("sbsa_kmeans_iterate", _lib.ptr(fit_bf), _lib.ptr(fit_f32), index_dim,
                           _lib.ptr(sample_idx), fit_n, cf, index_dim, _lib.ptr(assign_s),
                           _lib.ptr(sums_hist), _lib.ptr(counts_hist), _lib.ptr(no_restart),
-                          _lib.ptr(cent_f32), _lib.ptr(cent_bf), start, iters, s)
+                          _lib.ptr(restart_rows), k_ahead, _lib.ptr(restart_flags), _lib.ptr(cent_f32),
+                          _lib.ptr(cent_bf), _lib.ptr(member_bits), bits_bytes, i0, i1, s)
+            if fit_trace is not None:
+                for i in range(start, iters):
+                    entry = cent_bf.clone()
+                    call(i, i + 1)
+                    steps[i] = (entry, assign_s.clone())
+                return
+            if start < iters:
+                call(start, iters)
 
-        def first_empty(it0):
-            """The first iteration >= it0 that left a cluster empty, or -1 (one host read)."""
-            counts_host[it0:iters].copy_(counts_hist[it0:iters])
-            torch.cuda.current_stream(dev).synchronize()
+        def read_counts(it0):
+            """Copy the counts of iterations it0.. to the host; the event marks their arrival."""
+            counts_host[it0:iters].copy_(counts_hist[it0:iters], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            return ev
+
+        def empty_iterations(it0):
+            """The iterations >= it0 that left a cluster empty (the counts are on the host)."""
             hit = torch.nonzero((counts_host[it0:iters] == 0).any(dim=1)).flatten()
-            return it0 + int(hit[0]) if hit.numel() else -1
+            return [it0 + int(i) for i in hit]
 
-        draws = draw_sample_and_init()
-        for h in range(hkv):
-            kh = pk[:, h]
-            _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
-                      int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
-            sample_idx, init = draws
-            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(fit_f32),
-                      index_dim, _lib.ptr(sample_idx), cf, index_dim, _lib.ptr(cent_f32),
-                      _lib.ptr(cent_bf), s)
-            iterate(0, sample_idx)
-            it = first_empty(0) if iters > 0 else -1
-            while it >= 0:
-                # the reference's restart of the empty clusters at iteration it
-                # (flat_index.py:277-283), then the later iterations again
-                empty = counts_host[it] == 0
-                src = torch.full((cf,), -1, dtype=torch.int32)
-                torch.randperm(fit_n, generator=gen, out=host.sub)
-                src[empty] = host.sub[:int(empty.sum())].to(torch.int32)
-                src_d = src.to(dev)
-                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
-                          _lib.ptr(src_d), _lib.ptr(fit_f32), index_dim, _lib.ptr(sample_idx),
-                          cf, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
-                iterate(it + 1, sample_idx)
-                it = first_empty(it + 1) if it + 1 < iters else -1
-            # assign every key, lay the runs out, descriptor
+        def finalize(h):
+            """Assign every key, lay the runs out, write the descriptor."""
             _lib.call("sbsa_kmeans_assign", _lib.ptr(fit_bf), index_dim, None, n_fit,
                       _lib.ptr(cent_bf), cf, index_dim, _lib.ptr(assign_all[sink:]), s)
             fit_assign = None
@@ -284,6 +288,51 @@ class ProductPostingIndex:
             else:
                 _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
                           c, index_dim, None, _lib.ptr(codebooks[h]), s)
+            return fit_assign
+
+        sample_idx, init, restart_rows, before_restart = draw()
+        for h in range(hkv):
+            kh = pk[:, h]
+            _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
+                      int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
+            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(fit_f32),
+                      index_dim, _lib.ptr(sample_idx), cf, index_dim, _lib.ptr(cent_f32),
+                      _lib.ptr(cent_bf), s)
+            iterate(0, sample_idx, restart_rows)
+            counted = read_counts(0) if iters > 0 else None
+            # the final steps are enqueued now, and again if an empty iteration past
+            # those restarted on the GPU is redone below
+            fit_assign = finalize(h)
+            # The next head's draws wait for this head's counts: they follow the restart
+            # draws this head takes, and drawing ahead for a guessed outcome costs host
+            # time the GPU then waits for
+            if counted is not None:
+                counted.synchronize()
+            empties = empty_iterations(0) if iters > 0 else []
+            if len(empties) < k_ahead:
+                gen.set_state(before_restart[len(empties)])   # take back the unused draws
+            # the GPU restarted the first k_ahead empty iterations; the next is restarted here
+            it = empties[k_ahead] if len(empties) > k_ahead else -1
+            while it >= 0:
+                # the reference's restart of the empty clusters at iteration it
+                # (flat_index.py:277-283), then the later iterations again
+                empty = counts_host[it] == 0
+                src = torch.full((cf,), -1, dtype=torch.int32)
+                torch.randperm(fit_n, generator=gen, out=host.sub)
+                src[empty] = host.sub[:int(empty.sum())].to(torch.int32)
+                src_d = src.to(dev)
+                _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
+                          _lib.ptr(src_d), _lib.ptr(fit_f32), index_dim, _lib.ptr(sample_idx),
+                          cf, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+                iterate(it + 1, sample_idx)
+                if it + 1 < iters:
+                    read_counts(it + 1).synchronize()
+                    later = empty_iterations(it + 1)
+                    it = later[0] if later else -1
+                else:
+                    it = -1
+                if it < 0:
+                    fit_assign = finalize(h)
             if fit_trace is not None:
                 # copies (a tensor already on the host would otherwise be the reused buffer)
                 fit_trace.append(dict(
@@ -297,8 +346,7 @@ class ProductPostingIndex:
                     partition=assign_all.to('cpu', copy=True).long()))
                 steps.clear()
             if h + 1 < hkv:
-                # the next head's draws, on the host while the GPU lays this head out
-                draws = draw_sample_and_init()
+                sample_idx, init, restart_rows, before_restart = draw()
         width = int(totals.max().item())
         posting = posting_full[:, :width].contiguous()
         return cls(codebooks=codebooks, posting_positions=posting, bucket_indptr=indptr,

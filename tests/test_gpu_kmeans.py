@@ -217,15 +217,18 @@ def test_build_with_empty_clusters_matches_the_oracle():
 
 
 @pytest.mark.parametrize("dim", [256, 320])
-def test_update_sums_each_cluster_in_row_order(dim):
+def test_update_sums_and_counts_each_cluster(dim):
     """The centroid sums through the C-ABI on a skewed assignment: cluster 0 holds
-    most rows (more than the kernel lists before it sums), cluster 5 none, the row
-    count is ragged and the rows are read through a row map.  Each sum must equal the
-    sequential fp32 sum of its member rows in row order, bit for bit."""
-    import numpy as np
+    most rows (more than the kernel lists at once, so it is summed in windows),
+    cluster 5 none, the row count is ragged and the rows are read through a row map.
+    Counts exact; each sum within fp32 summation-order error of the fp64 sum of its
+    rows (the bound the fit's trace check uses); a second call on stale scratch gives
+    the same bits."""
     from semblo_amd import _lib
     gen = torch.Generator().manual_seed(11)
-    rows, n, c = 12000, 9000 + 37, 64
+    # ragged (not a multiple of 512 rows), two segments of 32768 rows, cluster 0 past the
+    # kernel's 8192-entry member list within one segment
+    rows, n, c = 48000, 40000 + 37, 64
     x = torch.randn(rows, dim, generator=gen)
     row_index = torch.randperm(rows, generator=gen)[:n].to(torch.int32)
     assign = torch.randint(1, c, (n,), generator=gen, dtype=torch.int32)
@@ -234,16 +237,21 @@ def test_update_sums_each_cluster_in_row_order(dim):
     xd, rd, ad = x.to(DEV), row_index.to(DEV), assign.to(DEV)
     sums = torch.full((c, dim), float("nan"), device=DEV)
     counts = torch.full((c,), -1, dtype=torch.int32, device=DEV)
+    nbytes = _lib.query("sbsa_kmeans_member_bits_bytes", n, c)
+    bits = torch.full((nbytes // 4,), -1, dtype=torch.int32, device=DEV)    # stale contents
     _lib.call("sbsa_kmeans_update", _lib.ptr(xd), dim, _lib.ptr(rd), n, _lib.ptr(ad), c, dim,
-              _lib.ptr(sums), _lib.ptr(counts), _lib.stream(xd.device))
+              _lib.ptr(sums), _lib.ptr(counts), _lib.ptr(bits), nbytes, _lib.stream(xd.device))
     torch.cuda.synchronize()
-    xs = x.numpy()[row_index.long().numpy()]
-    a = assign.numpy()
-    want = np.zeros((c, dim), np.float32)
-    for cl in range(c):
-        m = xs[a == cl]
-        if len(m):
-            want[cl] = np.cumsum(m, axis=0, dtype=np.float32)[-1]    # sequential, row order
-    assert int((a == 0).sum()) > 4096 and int((a == 5).sum()) == 0
-    assert torch.equal(counts.cpu(), torch.bincount(assign.long(), minlength=c).to(torch.int32))
-    assert np.array_equal(sums.cpu().numpy(), want)
+    first = sums.clone()
+    _lib.call("sbsa_kmeans_update", _lib.ptr(xd), dim, _lib.ptr(rd), n, _lib.ptr(ad), c, dim,
+              _lib.ptr(sums), _lib.ptr(counts), _lib.ptr(bits), nbytes, _lib.stream(xd.device))
+    torch.cuda.synchronize()
+    assert torch.equal(sums, first)
+    want = torch.zeros(c, dim, dtype=torch.float64).index_add_(0, assign.long(),
+                                                               x[row_index.long()].double())
+    cnt = torch.bincount(assign.long(), minlength=c)
+    assert int(cnt[:1]) > 2 * 8192 and int(cnt[5]) == 0
+    assert torch.equal(counts.cpu(), cnt.to(torch.int32))
+    scale = cnt.clamp_min(1).double()[:, None]
+    assert float(((sums.cpu().double() - want).abs() / scale).max()) <= 1e-5
+    assert torch.count_nonzero(sums[5]) == 0
