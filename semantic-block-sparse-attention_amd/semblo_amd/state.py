@@ -16,9 +16,13 @@ of empty clusters) come from a CPU ``torch.Generator`` seeded with
 keys' device; drawing on the CPU makes the partition independent of the
 device's RNG, and identical to the reference's own CPU build.  The
 reference reads the cluster counts every k-means iteration (its
-``empty.any()`` test); here the iterations run ahead and one read finds the
-first iteration that left a cluster empty, which is redone from there with
-the restart rows drawn, so the result is the same with fewer host reads.
+``empty.any()`` test).  Here the first RESTARTS_AHEAD restart draws of a head
+are made ahead and applied on the GPU at the first iterations that leave a
+cluster empty, the iterations run ahead, and one read of the counts tells
+how many draws were used: the generator's state is set back before the first
+unused one, and a later empty iteration is redone from there with its draw
+made then.  The draws and the result are the reference's, with one host read
+per head.
 
 With an attention sink (SEMBLO_SINK_TOKENS=S, state.py:757-782) positions
 0..S-1 form cluster 0, whose descriptor is zero, and the other positions are
