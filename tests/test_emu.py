@@ -68,3 +68,11 @@ def test_gpu_selection_and_append_tests_under_emulation():
     _run("gpu_tests", "test_gpu_select.py",
          "test_gpu_token_order.py::test_append_rows_bit_exact",
          "test_gpu_token_order.py::test_append_rows_flags_an_id_out_of_range", timeout=900)
+
+
+def test_kmeans_build_with_restarts_under_emulation():
+    """The index build on keys that leave clusters empty (restarts drawn ahead and
+    applied on the device, then on the host past two), run unchanged on the emulated
+    kernels: assignment, member bitmaps, sums and centroid steps under the sanitizer."""
+    _run("gpu_tests", "test_gpu_kmeans.py::test_build_with_empty_clusters_matches_the_oracle",
+         timeout=900)
