@@ -135,7 +135,8 @@ class ProductPostingIndex:
         ``fit_trace``, if given, receives one dict per KV head with the fit's
         intermediate states (the key space, the sample rows, and per iteration
         the centroids it starts from, its assignment, sums and counts; then the
-        final centroids and assignment of every key), for parity checks of each
+        final centroids and assignment of every key, and the sample rows drawn to
+        restart the clusters an iteration left empty), for parity checks of each
         k-means step.  The iterations then run one call at a time.  With a sink the
         fit covers positions S.. only, and so do the trace's rows, sample and final
         assignment (cluster ids 0..C-2 of that fit).
@@ -315,6 +316,11 @@ class ProductPostingIndex:
             empties = empty_iterations(0) if iters > 0 else []
             if len(empties) < k_ahead:
                 gen.set_state(before_restart[len(empties)])   # take back the unused draws
+            if fit_trace is not None:
+                # the sample rows each restarted iteration drew, for its empty clusters in
+                # ascending order (the GPU applied the first k_ahead of them)
+                drawn = {it: host.restarts[k][:int((counts_host[it] == 0).sum())].clone().long()
+                         for k, it in enumerate(empties[:k_ahead])}
             # the GPU restarted the first k_ahead empty iterations; the next is restarted here
             it = empties[k_ahead] if len(empties) > k_ahead else -1
             while it >= 0:
@@ -324,6 +330,8 @@ class ProductPostingIndex:
                 src = torch.full((cf,), -1, dtype=torch.int32)
                 torch.randperm(fit_n, generator=gen, out=host.sub)
                 src[empty] = host.sub[:int(empty.sum())].to(torch.int32)
+                if fit_trace is not None:
+                    drawn[it] = host.sub[:int(empty.sum())].clone().long()
                 src_d = src.to(dev)
                 _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
                           _lib.ptr(src_d), _lib.ptr(fit_f32), index_dim, _lib.ptr(sample_idx),
@@ -347,6 +355,7 @@ class ProductPostingIndex:
                     sums=sums_hist[:iters].to('cpu', copy=True), counts=counts_hist[:iters].to('cpu', copy=True),
                     final_centroids_f32=cent_f32.to('cpu', copy=True), final_centroids=cent_bf.to('cpu', copy=True),
                     final_assign=(fit_assign if sink else assign_all).to('cpu', copy=True).long(),
+                    restarts={it: d for it, d in drawn.items() if it < iters},
                     partition=assign_all.to('cpu', copy=True).long()))
                 steps.clear()
             if h + 1 < hkv:

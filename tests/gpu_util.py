@@ -187,6 +187,69 @@ def assignment_near_ties(x_bf16: torch.Tensor, cent_bf16: torch.Tensor, got: tor
     return int(rows.numel())
 
 
+def router_flip_margin(dim: int) -> float:
+    """Relative distance from a bf16 rounding midpoint within which two correct fp32 key
+    routers (x / max(||x||, 1e-12), routing_map.py:52-59) can round an element apart: the
+    fp32 sum of dim squares differs by at most dim * 2^-24 (relative) between summation
+    orders, the square root halves that, and the quotient adds one rounding (2^-24); the
+    bound is doubled."""
+    return 2.0 * (dim * 2.0 ** -25 + 2.0 ** -24)
+
+
+def check_key_router(k_pre: torch.Tensor, space_f32: torch.Tensor, space_bf16: torch.Tensor,
+                     tag: str = "") -> dict:
+    """The GPU key space of one KV head built with the router pass (sbsa_key_space with
+    router_pass=1) against the oracle, element by element.
+
+    k_pre [L, D] bf16 are the pre-RoPE keys; space_f32 / space_bf16 the GPU's routing space.
+    The GPU's bf16 router output r_gpu is recovered from its routing space: space_f32 is
+    r_gpu / ||r_gpu|| to fp32 rounding, and ||r_gpu|| equals the oracle's ||r_ref|| to
+    within a few 1e-5 (relative), far below the bf16 spacing, so rounding
+    space_f32 * ||r_ref|| to bf16 gives r_gpu exactly.  The recovery is then confirmed:
+    the oracle's routing space of r_gpu must equal space_f32 within 2e-6 in every row.
+
+    Every element where r_gpu differs from the oracle's r_ref = bf16(normalize(k)) must
+    itself be a rounding near-tie: the two values are adjacent bf16 numbers and the exact
+    quotient k / ||k|| (fp64) lies within router_flip_margin(D) (relative) of the midpoint
+    between them.  space_bf16 must be the bf16 rounding of the routing space of r_gpu up to
+    rounding near-ties.  Returns the counts of flipped elements, rows and bf16 space
+    values."""
+    import torch.nn.functional as F
+    kd = k_pre.cpu()
+    dim = kd.shape[-1]
+    r_ref = ref.routing_normalize_keys(kd)
+    n_ref = r_ref.double().norm(dim=-1, keepdim=True)
+    sf = space_f32.cpu()
+    r_gpu = (sf.double() * n_ref).float().to(torch.bfloat16)
+    s_gpu = F.normalize(ref.routing_space(r_gpu).float(), dim=-1)
+    off = (sf - s_gpu).abs().amax(-1)
+    assert float(off.max()) <= 2e-6, (
+        f"{tag}: the GPU key space is not the routing space of any bf16 router output "
+        f"(row {int(off.argmax())} off by {float(off.max()):.3g})")
+    diff = torch.nonzero(r_gpu != r_ref)
+    n_elem = int(diff.shape[0])
+    if n_elem:
+        rows, cols = diff[:, 0], diff[:, 1]
+        g = r_gpu[rows, cols]
+        w = r_ref[rows, cols]
+        gb = g.view(torch.int16).int()
+        wb = w.view(torch.int16).int()
+        adjacent = ((gb - wb).abs() == 1) & ((gb ^ wb) >= 0)
+        mid = 0.5 * (g.double() + w.double())
+        kr = kd[rows].double()
+        exact = kr[torch.arange(rows.numel()), cols] / kr.norm(dim=-1).clamp_min(1e-12)
+        near = (exact - mid).abs() <= router_flip_margin(dim) * mid.abs()
+        bad = ~(adjacent & near)
+        assert not bool(bad.any()), (
+            f"{tag}: {int(bad.sum())} of {n_elem} router elements differ from the oracle's "
+            f"without a rounding near-tie (first at row {int(rows[bad][0])}, dim "
+            f"{int(cols[bad][0])}: got {float(g[bad][0])!r}, want {float(w[bad][0])!r})")
+    n_space = bf16_rounding_near_ties(space_bf16.cpu(), s_gpu.to(torch.bfloat16),
+                                      [F.normalize(r_gpu.double(), dim=-1)], row_scaled=True)
+    return dict(router_elements=n_elem, router_rows=int(diff[:, 0].unique().numel()) if n_elem else 0,
+                space_flips=n_space)
+
+
 def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_final: torch.Tensor,
                     ref_final_centroids: torch.Tensor, tag: str = "",
                     k_pre_h: torch.Tensor | None = None) -> dict:
@@ -215,21 +278,16 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
     """
     import torch.nn.functional as F
     space_ref = F.normalize(ref.routing_space(product_h).float(), dim=-1)
-    exact_space = F.normalize(product_h.double(), dim=-1)
-    far = (gpu["space_f32"] - space_ref).abs().amax(-1) > 2e-6
-    n_router = int(far.sum())
-    if n_router:
-        # rows whose router output (bf16) differs: the GPU build normalised the pre-RoPE
-        # keys itself, and some element of the row must be a rounding near-tie there
-        assert k_pre_h is not None, f"{tag}: key space differs from the oracle's ({n_router} rows)"
-        r = F.normalize(k_pre_h[far].double(), dim=-1)
-        rms = r.pow(2).mean(-1, keepdim=True).sqrt()
-        near = (bf16_midpoint_gap(r) <= NEAR_TIE_REL * torch.maximum(r.abs(), rms)).any(-1)
-        assert bool(near.all()), \
-            f"{tag}: {int((~near).sum())} key rows differ with no router rounding near-tie"
-    keep = ~far
-    n_space = bf16_rounding_near_ties(gpu["space_bf16"][keep], space_ref.to(torch.bfloat16)[keep],
-                                      [exact_space[keep]], row_scaled=True)
+    if k_pre_h is not None:
+        # the GPU ran the router itself: element by element against the oracle's router
+        kr = check_key_router(k_pre_h, gpu["space_f32"], gpu["space_bf16"], tag)
+        n_router, n_router_rows, n_space = kr["router_elements"], kr["router_rows"], kr["space_flips"]
+    else:
+        off = (gpu["space_f32"] - space_ref).abs().amax(-1)
+        assert float(off.max()) <= 2e-6, f"{tag}: key space differs from the oracle's"
+        n_router = n_router_rows = 0
+        n_space = bf16_rounding_near_ties(gpu["space_bf16"], space_ref.to(torch.bfloat16),
+                                          [F.normalize(product_h.double(), dim=-1)], row_scaled=True)
     sample = gpu["sample"]
     xs_bf = gpu["space_bf16"][sample]
     xs_f32 = gpu["space_f32"][sample]
@@ -239,7 +297,7 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
     def onehot_sums64(x, assign):
         return torch.zeros(c, x.shape[1], dtype=torch.float64).index_add_(0, assign, x.double())
 
-    flips_assign = flips_cent = 0
+    flips_assign = flips_cent = restarted = 0
     origin = int((xs_bf != xs_ref.to(torch.bfloat16)).any(-1).sum())   # sample rows whose bf16 differs
     on_track = origin == 0
     first_departure = -1
@@ -276,6 +334,18 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
                                               [exact_entry[live],
                                                F.normalize(onehot_sums64(xs_f32, a_gpu) / scale,
                                                            dim=-1)[live]], row_scaled=True)
+        if not bool(live.all()):
+            # the empty clusters restart on the sample rows the generator drew, in ascending
+            # cluster order (flat_index.py:277-283): centroid = normalize(sample row)
+            draws = gpu.get("restarts", {}).get(i)
+            assert draws is not None and draws.numel() == int((~live).sum()), \
+                f"{tag}: iteration {i} left {int((~live).sum())} clusters empty, trace has draws {draws}"
+            rows = xs_f32[draws]
+            exact_entry[~live] = F.normalize(xs_ref[draws].double(), dim=-1)
+            flips_cent += bf16_rounding_near_ties(
+                nxt[~live], F.normalize(rows, dim=-1).to(torch.bfloat16),
+                [F.normalize(rows.double(), dim=-1), exact_entry[~live]], row_scaled=True)
+            restarted += int((~live).sum())
     if on_track:
         n = bf16_rounding_near_ties(gpu["final_centroids"], ref_final_centroids.to(torch.bfloat16),
                                     [exact_entry], row_scaled=True)
@@ -284,9 +354,44 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
     flips_final = assignment_near_ties(gpu["space_bf16"], gpu["final_centroids"],
                                        gpu["final_assign"], fin)
     moved = int((gpu["final_assign"] != ref_final).sum())
-    rep = dict(router_flips=n_router, space_flips=n_space, assign_flips=flips_assign, centroid_flips=flips_cent,
+    # The oracle's fit run on the GPU's own key space (which differs from the oracle's only
+    # at the near-ties counted above) from the GPU's first centroids, with the GPU's restart
+    # draws: it must follow the GPU's trajectory exactly unless an assignment or centroid
+    # near-tie was counted inside the loop, and then end in the GPU's final membership up
+    # to the final near-ties.  This accounts for every key that ``moved`` against the
+    # oracle's own run.
+    shadow_departure = -1
+    cent_bf = gpu["entry_centroids"][0]
+    for i in range(iters):
+        a = ref.argmax_sim_chunked(xs_bf.float(), cent_bf.float(), 65536)
+        if not torch.equal(a, gpu["assign"][i]):
+            shadow_departure = i
+            break
+        counts = torch.bincount(a, minlength=c)
+        sums = ref.segment_sum_matmul(xs_f32, a, c)
+        empty = counts == 0
+        if bool(empty.any()):
+            sums[empty] = xs_f32[gpu["restarts"][i]]
+            counts[empty] = 1
+        cent = F.normalize(sums / counts[:, None].float(), dim=-1)
+        cent_bf = cent.to(torch.bfloat16)
+        nxt = gpu["entry_centroids"][i + 1] if i + 1 < iters else gpu["final_centroids"]
+        if not torch.equal(cent_bf, nxt):
+            shadow_departure = i + 1
+            break
+    if flips_assign == 0 and flips_cent == 0:
+        assert shadow_departure < 0, (
+            f"{tag}: the GPU's fit leaves the oracle's run on its own key space at iteration "
+            f"{shadow_departure} with no near-tie counted inside the loop")
+    shadow_moved = None
+    if shadow_departure < 0:
+        shadow_final = ref.argmax_sim_chunked(gpu["space_bf16"].float(), cent_bf.float(), 65536)
+        shadow_moved = int((gpu["final_assign"] != shadow_final).sum())
+        assert shadow_moved <= flips_final, f"{tag}: {shadow_moved} keys moved against the shadow run"
+    rep = dict(router_flips=n_router, router_rows=n_router_rows, space_flips=n_space,
+               assign_flips=flips_assign, centroid_flips=flips_cent, restarted=restarted,
                final_flips=flips_final, origin_flips=origin, first_departure=first_departure,
-               moved=moved)
+               shadow_departure=shadow_departure, shadow_moved=shadow_moved, moved=moved)
     if origin == 0:
         assert first_departure < 0, f"{tag}: left the oracle's trajectory at no near-tie: {rep}"
         # the same final centroids: keys outside the sample differ only at final near-ties

@@ -75,3 +75,94 @@ def test_last_index_tie_break_fails():
     if bool((gaps > 1e-4).any()):
         with pytest.raises(AssertionError):
             assignment_near_ties(x, cb, last, first)
+
+
+def _router_space(r: torch.Tensor):
+    """The GPU build's key space of a bf16 router output r: two fp32 normalisations."""
+    s = F.normalize(F.normalize(r.float(), dim=-1), dim=-1)
+    return s, s.to(torch.bfloat16)
+
+
+def _reordered_router(k: torch.Tensor) -> torch.Tensor:
+    """A key router that sums the squares in another order than torch's (pairwise halves,
+    then the halves reversed), as a GPU wave reduction does."""
+    x = k.float()
+    ss = x.pow(2)
+    while ss.shape[-1] > 1:
+        h = ss.shape[-1] // 2
+        ss = ss[..., h:] + ss[..., :h]
+    n = ss.sqrt().clamp_min(1e-12)
+    return (x / n).to(torch.bfloat16)
+
+
+def test_key_router_check_accepts_a_reordered_router():
+    from gpu_util import check_key_router
+    gen = torch.Generator().manual_seed(5)
+    k = (torch.randn(4096, 256, generator=gen) * 3).to(torch.bfloat16)
+    r = _reordered_router(k)
+    s32, s16 = _router_space(r)
+    rep = check_key_router(k, s32, s16, "reordered")
+    assert rep["router_elements"] == int((r != ref.routing_normalize_keys(k)).sum())
+
+
+def test_key_router_check_rejects_a_flip_that_is_not_a_near_tie():
+    """One element one bf16 step off, in a row that also holds a true rounding near-tie
+    elsewhere: the element itself must be the near-tie, so the check fails."""
+    from gpu_util import check_key_router, router_flip_margin
+    gen = torch.Generator().manual_seed(6)
+    k = (torch.randn(512, 128, generator=gen)).to(torch.bfloat16)
+    r = ref.routing_normalize_keys(k).clone()
+    exact = F.normalize(k.double(), dim=-1)
+    gap = bf16_midpoint_gap(exact) / exact.abs().clamp_min(1e-30)
+    row = int(torch.nonzero((gap < router_flip_margin(128)).any(-1))[0]) if bool(
+        (gap < router_flip_margin(128)).any()) else 0
+    col = int(gap[row].argmax())                        # the element farthest from a midpoint
+    bits = r.view(torch.int16)
+    bits[row, col] += 1
+    s32, s16 = _router_space(r)
+    with pytest.raises(AssertionError, match="without a rounding near-tie"):
+        check_key_router(k, s32, s16, "corrupt")
+
+
+def test_key_router_check_rejects_a_space_that_no_router_output_gives():
+    from gpu_util import check_key_router
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn(256, 64, generator=gen).to(torch.bfloat16)
+    s32, s16 = _router_space(ref.routing_normalize_keys(k))
+    s32 = s32.clone()
+    s32[9, 3] += 1e-5
+    with pytest.raises(AssertionError, match="not the routing space"):
+        check_key_router(k, s32, s16, "space")
+
+
+def test_restarted_cluster_must_take_its_drawn_row():
+    """An iteration that leaves a cluster empty restarts it on the drawn sample row; a
+    trace whose next centroid for it is another row fails."""
+    gen = torch.Generator().manual_seed(23)
+    length, d = 1024, 64
+    dirs = torch.randn(5, d, generator=gen)
+    k = dirs[torch.randint(0, 5, (length,), generator=gen)] + 1e-3 * torch.randn(length, d, generator=gen)
+    product = ref.routing_normalize_keys(k[:, None].to(torch.bfloat16))
+    steps, draws = [], []
+    ref.build_flat_index(product, codebook_seed=5, fit_steps=steps, traces=draws)
+    st = steps[0]
+    space = F.normalize(ref.routing_space(product[:, 0]).float(), dim=-1)
+    sample = [x[1] for x in draws[0] if x[0] == "sample"][0]
+    empties = [x[1] for x in draws[0] if x[0] == "empty"]
+    restarts = {i: e for i, e in enumerate(empties) if e.numel()}
+    assert restarts, "the fit must leave a cluster empty"
+    tr = dict(space_f32=space, space_bf16=space.to(torch.bfloat16), sample=sample,
+              entry_centroids=[s["entry"].to(torch.bfloat16) for s in st["steps"]],
+              assign=[s["assign"] for s in st["steps"]],
+              sums=torch.stack([s["sums"] for s in st["steps"]]),
+              counts=torch.stack([s["counts"].to(torch.int32) for s in st["steps"]]),
+              final_centroids_f32=st["final_centroids"],
+              final_centroids=st["final_centroids"].to(torch.bfloat16),
+              final_assign=st["final_assign"].clone(), restarts=restarts)
+    rep = check_fit_trace(product[:, 0], tr, st["steps"], st["final_assign"], st["final_centroids"])
+    assert rep["restarted"] == sum(int(e.numel()) for e in restarts.values())
+    assert rep["shadow_departure"] == -1 and rep["shadow_moved"] == 0
+    it = min(restarts)
+    bad = dict(tr, restarts={**restarts, it: (restarts[it] + 1) % sample.numel()})
+    with pytest.raises(AssertionError):
+        check_fit_trace(product[:, 0], bad, st["steps"], st["final_assign"], st["final_centroids"])
