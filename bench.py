@@ -405,7 +405,8 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
                         log_uniform=conf["log_uniform"], sinks=conf["sinks"], seed=0,
                         dtype=torch.bfloat16, device="cuda")
     cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
-                              query_chunk_size=conf["chunk"], suffix_reserve=max(1024, dsteps + 16))
+                              query_chunk_size=conf["chunk"],
+                              suffix_shuffle_seed=5 if conf.get("shuffle_suffix") else None)
     if args.decode_splits:
         cfg.decode_num_splits = max(1, args.decode_splits - cfg.decode_suffix_splits)
     layer = SembloAttention(cfg, layer_name=f"bench.layer.{config}")

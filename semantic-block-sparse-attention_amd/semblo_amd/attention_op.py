@@ -26,8 +26,8 @@ def register_layer(layer_name: str, layer: Any) -> None:
 def registered_layer(layer_name: str) -> Any:
     layer = _LAYERS.get(str(layer_name))
     if layer is None:
-        raise RuntimeError(f"no semblo layer is registered as {layer_name!r}; the operator is "
-                           "reachable only through a layer that registered itself")
+        raise RuntimeError(f"layer name {layer_name!r} is unknown to semblo::attention: "
+                           "construct its SembloAttention (which calls register_layer) first")
     return layer
 
 

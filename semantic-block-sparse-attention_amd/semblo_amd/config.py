@@ -7,7 +7,7 @@ power-of-two cluster count).
 from __future__ import annotations
 
 import os
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 PAGE = 16                    # SEMBLO_FA3_BODY / SEMBLO_FA3_ALIGN
 FLAT_UNIT_TOKENS = 2048      # SEMBLO_FLAT_UNIT_TOKENS
@@ -37,6 +37,18 @@ def check_sink_partition(sink: int, length: int, fit_length: int, num_clusters: 
     if length <= sink or fit_length - sink < 2 * num_clusters:
         raise RuntimeError(f"SEMBLO_SINK_TOKENS={sink} leaves too few keys ({length:,} in the prompt, "
                            f"{fit_length:,} to fit) for {num_clusters - 1} clusters")
+
+
+def default_suffix_reserve(room: int | None = None) -> int:
+    """Generated positions a layer's decode state holds room for (arena.py:50-63):
+    SEMBLO_SUFFIX_RESERVE if set, else the model's room for generated tokens capped at
+    65,536, else 65,536."""
+    env = os.environ.get("SEMBLO_SUFFIX_RESERVE")
+    if env is not None:
+        return int(env)
+    if room is not None:
+        return max(1, min(65536, int(room)))
+    return 65536
 
 
 def num_flat_clusters(length: int, unit_tokens: int = FLAT_UNIT_TOKENS,
@@ -71,8 +83,10 @@ class SembloRuntimeConfig:
                                             # 64 blocks per KV head)
     decode_suffix_splits: int = 8           # SEMBLO_DECODE_SUFFIX_SPLITS
     suffix_block: int = 256
-    suffix_reserve: int = 1024
+    suffix_reserve: int = field(default_factory=lambda: default_suffix_reserve())
     sm_scale: float | None = None           # None: head_dim ** -0.5
+    suffix_shuffle_seed: int | None = None  # suffix blocks in a shuffled physical order (a paged
+                                            # cache's page order); None: in order
 
     @property
     def scale(self) -> float:

@@ -128,8 +128,10 @@ class SembloAttention:
         cfg = self.runtime_config
         index.original_kv = None
         self.index = index
+        shuffle = None if cfg.suffix_shuffle_seed is None else \
+            torch.Generator().manual_seed(int(cfg.suffix_shuffle_seed))
         self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
-                                 suffix_splits=cfg.decode_suffix_splits)
+                                 suffix_splits=cfg.decode_suffix_splits, shuffle_blocks=shuffle)
 
     def prefill_token_order(self, q_post, q_pre, k_pre, k_post, v, output, chunk: int,
                             timing=None, store_timing=None, **kw) -> torch.Tensor:

@@ -97,7 +97,7 @@ class StreamedPrefillSession:
         hq, d = layer.num_heads, layer.head_dim
         n = q_post.shape[0]
         start = int(start)
-        if not 0 <= start and start + n <= self.tokens:
+        if not (0 <= start and start + n <= self.tokens):
             raise ValueError(f"queries [{start}, {start + n}) outside the prompt of {self.tokens}")
         q = q_post.reshape(n, hq, d)
         qp = q_pre.reshape(n, hq, d)

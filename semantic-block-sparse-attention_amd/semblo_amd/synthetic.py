@@ -85,7 +85,7 @@ CONFIGS = {
     1: dict(length=8192, hq=8, hkv=2, d=128, mixtures=64, seg=(32, 256), log_uniform=False,
             sinks=0, dtype=torch.float32, chunk=8192, decode_steps=16),
     2: dict(length=32768, hq=16, hkv=4, d=256, mixtures=256, seg=(32, 256), log_uniform=False,
-            sinks=0, dtype=torch.bfloat16, chunk=8192, decode_steps=64),
+            sinks=0, dtype=torch.bfloat16, chunk=8192, decode_steps=64, shuffle_suffix=True),
     3: dict(length=131072, hq=16, hkv=4, d=256, mixtures=1024, seg=(16, 2048), log_uniform=True,
             sinks=4, dtype=torch.bfloat16, chunk=8192, decode_steps=256),
     4: dict(length=524288, hq=16, hkv=4, d=256, mixtures=1024, seg=(16, 2048), log_uniform=True,

@@ -474,6 +474,11 @@ def check_recorded_chunk(rec: dict, q: torch.Tensor, q_pre: torch.Tensor, k: tor
     at counted near-ties).  q, q_pre, k, v, out: CPU tensors of the whole prompt."""
     cs, ce, wstart = rec["chunk_start"], rec["chunk_end"], rec["wstart"]
     sizes = rec["causal_sizes"].cpu()
+    # the chunk's size snapshot is the snapshot rule at its window start
+    # (CausalSnapshot.advance, fused_prefill.py:126-135)
+    snap = ref.causal_sizes_at(index.posting_positions.cpu(), index.bucket_indptr.cpu(),
+                               index.bucket_sizes.cpu(), wstart)
+    assert torch.equal(sizes, snap), f"{tag} chunk {cs}: causal sizes differ from the snapshot at {wstart}"
     hkv, c = sizes.shape
     qmask = rec["qmask"].cpu()
     n = ce + 1 - cs

@@ -42,3 +42,20 @@ def test_reserved_layout_matches_the_oracle_bit_for_bit(align):
         if want is not None:
             assert got.dtype == torch.int64 and torch.equal(got, want), (t, hkv, c, width)
     assert 0 < refused < 300          # both outcomes were exercised
+
+
+def test_streamed_queries_refuse_a_slice_past_the_prompt():
+    """StreamedPrefillSession.queries refuses positions outside [0, tokens) before it
+    touches a device (model.py:1509-1524 takes slices inside the prompt only)."""
+    import types
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.streamed_prefill import StreamedPrefillSession
+    cfg = SembloRuntimeConfig(num_q_heads=4, num_kv_heads=1, head_dim=64)
+    layer = types.SimpleNamespace(runtime_config=cfg, num_heads=4, num_kv_heads=1, head_dim=64,
+                                  target_tokens=0, index=None, arena=None)
+    session = StreamedPrefillSession(layer, 100)
+    session.index = object()                 # past ingest
+    q = torch.zeros(8, 4, 64, dtype=torch.bfloat16)
+    for start in (95, -1, 100):
+        with pytest.raises(ValueError, match="outside the prompt"):
+            session.queries(q, q, start)
