@@ -298,6 +298,7 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
         return torch.zeros(c, x.shape[1], dtype=torch.float64).index_add_(0, assign, x.double())
 
     flips_assign = flips_cent = restarted = 0
+    assign_at, cent_at = [], []             # near-ties counted at each iteration
     origin = int((xs_bf != xs_ref.to(torch.bfloat16)).any(-1).sum())   # sample rows whose bf16 differs
     on_track = origin == 0
     first_departure = -1
@@ -315,6 +316,7 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
         a_ref = ref.argmax_sim_chunked(xs_bf.float(), cin.float(), 65536)
         n = assignment_near_ties(xs_bf, cin, a_gpu, a_ref)
         flips_assign += n
+        assign_at.append(n)
         if on_track:
             origin += n
             on_track = n == 0
@@ -330,6 +332,7 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
         nxt = gpu["entry_centroids"][i + 1] if i + 1 < iters else gpu["final_centroids"]
         cent = F.normalize(sums / counts.clamp_min(1)[:, None].float(), dim=-1)
         exact_entry = F.normalize(onehot_sums64(xs_ref, a_gpu) / scale, dim=-1)
+        cent_before = flips_cent
         flips_cent += bf16_rounding_near_ties(nxt[live], cent[live].to(torch.bfloat16),
                                               [exact_entry[live],
                                                F.normalize(onehot_sums64(xs_f32, a_gpu) / scale,
@@ -346,6 +349,7 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
                 nxt[~live], F.normalize(rows, dim=-1).to(torch.bfloat16),
                 [F.normalize(rows.double(), dim=-1), exact_entry[~live]], row_scaled=True)
             restarted += int((~live).sum())
+        cent_at.append(flips_cent - cent_before)
     if on_track:
         n = bf16_rounding_near_ties(gpu["final_centroids"], ref_final_centroids.to(torch.bfloat16),
                                     [exact_entry], row_scaled=True)
@@ -356,42 +360,40 @@ def check_fit_trace(product_h: torch.Tensor, gpu: dict, ref_steps: list, ref_fin
     moved = int((gpu["final_assign"] != ref_final).sum())
     # The oracle's fit run on the GPU's own key space (which differs from the oracle's only
     # at the near-ties counted above) from the GPU's first centroids, with the GPU's restart
-    # draws: it must follow the GPU's trajectory exactly unless an assignment or centroid
-    # near-tie was counted inside the loop, and then end in the GPU's final membership up
-    # to the final near-ties.  This accounts for every key that ``moved`` against the
-    # oracle's own run.
-    shadow_departure = -1
+    # draws.  Where its state differs from the GPU's, the iteration must hold a counted
+    # near-tie of that kind, and the run then continues from the GPU's state (a re-seed).
+    # It ends in the GPU's final centroids, and every key's final cluster must then be the
+    # GPU's up to the final near-ties.  So each key that ``moved`` against the oracle's own
+    # run is downstream of a counted near-tie, at an iteration the report names.
+    reseeds = []
     cent_bf = gpu["entry_centroids"][0]
     for i in range(iters):
         a = ref.argmax_sim_chunked(xs_bf.float(), cent_bf.float(), 65536)
         if not torch.equal(a, gpu["assign"][i]):
-            shadow_departure = i
-            break
+            assert assign_at[i] > 0, (f"{tag}: iteration {i}: the GPU's assignment differs from the "
+                                      f"oracle's on the same inputs with no near-tie counted")
+            reseeds.append(f"assign@{i}")
+            a = gpu["assign"][i]
         counts = torch.bincount(a, minlength=c)
         sums = ref.segment_sum_matmul(xs_f32, a, c)
         empty = counts == 0
         if bool(empty.any()):
             sums[empty] = xs_f32[gpu["restarts"][i]]
             counts[empty] = 1
-        cent = F.normalize(sums / counts[:, None].float(), dim=-1)
-        cent_bf = cent.to(torch.bfloat16)
+        cent_bf = F.normalize(sums / counts[:, None].float(), dim=-1).to(torch.bfloat16)
         nxt = gpu["entry_centroids"][i + 1] if i + 1 < iters else gpu["final_centroids"]
         if not torch.equal(cent_bf, nxt):
-            shadow_departure = i + 1
-            break
-    if flips_assign == 0 and flips_cent == 0:
-        assert shadow_departure < 0, (
-            f"{tag}: the GPU's fit leaves the oracle's run on its own key space at iteration "
-            f"{shadow_departure} with no near-tie counted inside the loop")
-    shadow_moved = None
-    if shadow_departure < 0:
-        shadow_final = ref.argmax_sim_chunked(gpu["space_bf16"].float(), cent_bf.float(), 65536)
-        shadow_moved = int((gpu["final_assign"] != shadow_final).sum())
-        assert shadow_moved <= flips_final, f"{tag}: {shadow_moved} keys moved against the shadow run"
+            assert cent_at[i] > 0, (f"{tag}: iteration {i}: the GPU's next centroids differ from "
+                                    f"the oracle's on the same inputs with no near-tie counted")
+            reseeds.append(f"centroids@{i}")
+            cent_bf = nxt
+    shadow_final = ref.argmax_sim_chunked(gpu["space_bf16"].float(), cent_bf.float(), 65536)
+    shadow_moved = int((gpu["final_assign"] != shadow_final).sum())
+    assert shadow_moved <= flips_final, f"{tag}: {shadow_moved} keys moved against the shadow run"
     rep = dict(router_flips=n_router, router_rows=n_router_rows, space_flips=n_space,
                assign_flips=flips_assign, centroid_flips=flips_cent, restarted=restarted,
                final_flips=flips_final, origin_flips=origin, first_departure=first_departure,
-               shadow_departure=shadow_departure, shadow_moved=shadow_moved, moved=moved)
+               shadow_reseeds=reseeds, shadow_moved=shadow_moved, moved=moved)
     if origin == 0:
         assert first_departure < 0, f"{tag}: left the oracle's trajectory at no near-tie: {rep}"
         # the same final centroids: keys outside the sample differ only at final near-ties

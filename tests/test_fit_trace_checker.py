@@ -161,7 +161,7 @@ def test_restarted_cluster_must_take_its_drawn_row():
               final_assign=st["final_assign"].clone(), restarts=restarts)
     rep = check_fit_trace(product[:, 0], tr, st["steps"], st["final_assign"], st["final_centroids"])
     assert rep["restarted"] == sum(int(e.numel()) for e in restarts.values())
-    assert rep["shadow_departure"] == -1 and rep["shadow_moved"] == 0
+    assert rep["shadow_reseeds"] == [] and rep["shadow_moved"] == 0
     it = min(restarts)
     bad = dict(tr, restarts={**restarts, it: (restarts[it] + 1) % sample.numel()})
     with pytest.raises(AssertionError):
