@@ -236,6 +236,9 @@ __global__ __launch_bounds__(1024) void append_rows_kernel(
             if (pass) rows[(int64_t)h * n + p] = start + __popcll(m & below);
             pending = false;
           }
+          // every lane has read mine[lid] before the lead lane adds to it (in
+          // order on the GPU; the barrier keeps the compiler from moving them)
+          __builtin_amdgcn_wave_barrier();
           if (lane == lead) mine[lid] += __popcll(m);
         }
       }

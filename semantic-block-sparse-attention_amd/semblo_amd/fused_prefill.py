@@ -111,10 +111,12 @@ def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, 
     return ChunkPlan(chunk_start, chunk_end, wstart, causal_sizes, tokens, kv, theta)
 
 
-def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int, *, sm_scale: float,
-                        fa3_page_size: int = 16, out: torch.Tensor | None = None, timing=None,
-                        window_kv=None) -> torch.Tensor:
-    """The attention of a planned sparse chunk, given its partial count ``nnz``."""
+def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int | None = None, *,
+                        sm_scale: float, fa3_page_size: int = 16, out: torch.Tensor | None = None,
+                        timing=None, window_kv=None) -> torch.Tensor:
+    """The attention of a planned sparse chunk.  ``nnz`` (its partial count, read on the
+    host) sizes the partial rows exactly; None sizes them by the capacity bound, so
+    the chunk is enqueued without waiting for its plan (kv_outer_execute)."""
     q_count, hq, d = q_chunk.shape
     hkv = index.num_kv_heads
     wstart, chunk_start, chunk_end = plan.wstart, plan.chunk_start, plan.chunk_end
@@ -181,8 +183,8 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
                             queries_per_block=queries_per_block, iters=iters, local=local,
                             dense_prefix_x=dense_prefix_x, keep_theta=plan_log is not None)
     plan.record(plan_log)
-    nnz = int(plan.kv.nnz_d.item())               # the one host read of the chunk
-    return fused_chunk_execute(plan, q_chunk, index, nnz, sm_scale=sm_scale,
+    # no host read: the partial rows are sized by the capacity bound
+    return fused_chunk_execute(plan, q_chunk, index, None, sm_scale=sm_scale,
                                fa3_page_size=fa3_page_size, out=out, timing=timing,
                                window_kv=window_kv)
 

@@ -67,6 +67,16 @@ def theta_select_bitmask_flat(vectors: torch.Tensor, logmix: torch.Tensor | None
     for t in (bitmask, qmask):
         if t is not None and (t.dtype != torch.int32 or not t.is_contiguous()):
             raise ValueError("bitmask / qmask must be contiguous int32")
+    # query q belongs to block q // g_union: its sizes row (unless broadcast) and its bitmask row
+    nb = (q + int(g_union) - 1) // max(int(g_union), 1)
+    if causal_sizes.shape[0] > 1 and causal_sizes.shape[0] < nb:
+        raise ValueError(f"causal_sizes has {causal_sizes.shape[0]} query blocks; {q} queries in "
+                         f"blocks of {g_union} need {nb}")
+    if bitmask is not None and (bitmask.shape[0] < nb or tuple(bitmask.shape[1:]) != (hkv, c // 32)):
+        raise ValueError(f"bitmask {tuple(bitmask.shape)} must be [{nb}, {hkv}, {c // 32}] for {q} "
+                         f"queries in blocks of {g_union}")
+    if qmask is not None and tuple(qmask.shape) != (q, hkv, c // 32):
+        raise ValueError(f"qmask {tuple(qmask.shape)} must be [{q}, {hkv}, {c // 32}]")
     _lib.call("sbsa_score_select", _lib.ptr(v), v.stride(0), v.stride(1), _lib.ptr(lm),
               _lib.ptr(cb), _lib.ptr(causal_sizes), s_nb, causal_sizes.stride(1), q, hq, hkv, c,
               dim, int(g_union), 1.0 / float(temperature), float(beta), float(target_tokens),

@@ -118,12 +118,21 @@ def kv_outer_plan(qmask: torch.Tensor, causal_sizes: torch.Tensor, *, num_querie
     return KVOuterPlan(qmask, nvis, qvals, counts, rev_indptr, nnz_d, qrank)
 
 
-def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan, nnz: int,
+def partials_capacity(num_queries: int, num_kv_heads: int, num_clusters: int) -> int:
+    """A bound of a chunk's partial count known without reading the device: a query
+    selects at most every cluster of each KV head (one partial per selected,
+    visible (query, KV head, cluster))."""
+    return int(num_queries) * int(num_kv_heads) * int(num_clusters)
+
+
+def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan, nnz: int | None,
                      bucket_indptr: torch.Tensor, *, sm_scale: float, local_kv, chunk_start: int,
                      wstart: int, out: torch.Tensor | None = None, want_stats: bool = False,
                      grid: int | None = None, timing=None):
     """The work list, the attention and the combine of one chunk, given its plan and
-    its partial count ``nnz`` (read on the host)."""
+    its partial count ``nnz`` read on the host, or None: the partial rows are then
+    sized by ``partials_capacity`` and nothing waits for the plan on the host (the
+    kernels take the count and the entries from the plan's device arrays)."""
     qn, hq, d = q.shape
     hkv = packed_kv.shape[2]
     g = hq // hkv
@@ -132,12 +141,13 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     c = qmask.shape[2] * 32
     dev = q.device
     k_loc, v_loc = local_kv
-    part_o = torch.empty(max(nnz, 1), g, d, dtype=q.dtype, device=dev)
-    part_lse = torch.empty(max(nnz, 1), g, dtype=torch.float32, device=dev)
+    cap = nnz if nnz is not None else partials_capacity(qn, hkv, c)
+    part_o = torch.empty(max(cap, 1), g, d, dtype=q.dtype, device=dev)
+    part_lse = torch.empty(max(cap, 1), g, dtype=torch.float32, device=dev)
     local_o = torch.empty_like(q)
     local_lse = torch.empty(qn, hq, dtype=torch.float32, device=dev)
     qt = queries_per_item(g)
-    bound = _lib.query("sbsa_prefill_items_bound", nnz, qn, hkv, c, qt)
+    bound = _lib.query("sbsa_prefill_items_bound", cap, qn, hkv, c, qt)
     items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
     queue = torch.empty(QUEUE_HEAD + max(bound, 1), dtype=torch.int32, device=dev)
     s = _lib.stream(dev)

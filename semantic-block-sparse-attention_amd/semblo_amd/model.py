@@ -89,17 +89,6 @@ class SembloAttention:
             self._side_stream = st
         return st
 
-    def _pinned_counts(self, n: int) -> torch.Tensor:
-        """Pinned host slots for the sparse chunks' partial counts, kept across
-        calls: a pinned allocation per call can stall the host while earlier
-        copies are still pending.  A call reads each slot only after its own
-        copy has landed."""
-        buf = getattr(self, "_nnz_host", None)
-        if buf is None or buf.numel() < max(n, 1):
-            buf = torch.empty(max(n, 64), dtype=torch.int64, pin_memory=True)
-            self._nnz_host = buf
-        return buf
-
     def begin_token_outer_prefill(self, tokens: int, chunk: int, **kw):
         """A token-order prefill session of ``tokens`` positions in slices of ``chunk``
         (the reference's layer.begin_token_outer_prefill, streamed_prefill.py:563-564)."""
@@ -169,11 +158,10 @@ class SembloAttention:
         side.wait_event(inputs_ready)
         sparse = [(st, min(length, st + step)) for st in range(0, length, step) if st > cap]
         # every sparse chunk's selection and reverse index on the build stream,
-        # each followed by a copy of its partial count to pinned host memory and
-        # an event.  Plans are enqueued one chunk ahead of the attention: a
-        # chunk's attention starts as soon as its own plan is done, and the
-        # next plan runs beside it.
-        nnz_host = self._pinned_counts(len(sparse))
+        # each followed by an event; a chunk's attention waits for its own plan
+        # on the GPU only.  Its partial rows are sized by the capacity bound
+        # (kv_outer.partials_capacity), so the host reads nothing and every
+        # chunk is enqueued at once.
         plans, ready = [], []
         with torch.cuda.stream(side):
             index = self._ingest_prompt_kv(kp, kk, vv)
@@ -188,20 +176,16 @@ class SembloAttention:
                                       iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x,
                                       keep_theta=self.plan_log is not None)
                 pl.record(self.plan_log)
-                nnz_host[i:i + 1].copy_(pl.kv.nnz_d, non_blocking=True)
                 ev = torch.cuda.Event()
                 ev.record(side)
             plans.append(pl)
             ready.append(ev)
 
         self.index = index
-        if sparse:
-            enqueue_plan(0)
+        for i in range(len(sparse)):
+            enqueue_plan(i)
         for i, (st, en) in enumerate(sparse):
-            if i + 1 < len(sparse):
-                enqueue_plan(i + 1)
             pl = plans[i]
-            ready[i].synchronize()          # this chunk's partial count is on the host
             main.wait_event(ready[i])
             if i == 0:
                 for t in (index.codebooks, index.posting_positions, index.bucket_indptr,
@@ -209,7 +193,7 @@ class SembloAttention:
                     t.record_stream(main)
             for t in pl.tensors():
                 t.record_stream(main)
-            fused_chunk_execute(pl, q[st:en], index, int(nnz_host[i]),
+            fused_chunk_execute(pl, q[st:en], index, None,
                                 sm_scale=self.scaling, out=out[st:en], timing=timing)
         built = torch.cuda.Event()
         built.record(side)

@@ -29,6 +29,10 @@ does (token_outer_prefill.py:155-159).
 Host reads: one per appended slice (the overflow flags, the reference's
 ``bool((sizes + counts > reserve).any())``), and the cluster sizes at the
 fit and at a repack, from which the reserved layout is computed on the host.
+They arrive by an asynchronous copy into pinned memory.  A sparse slice reads
+no row of its own slice from the store, so its attention is enqueued between
+the assignment and that read: the GPU runs it while the host waits for the
+flags and lays out any repack, which then follows the attention on the stream.
 """
 from __future__ import annotations
 
@@ -171,12 +175,22 @@ class TokenOuterPrefillSession:
         self.index: ProductPostingIndex | None = None
         self.snapshot: TokenOuterSnapshot | None = None
         self.reserve: torch.Tensor | None = None
+        self._reserve_dev: torch.Tensor | None = None
         self.repacks = 0
         self.repacks_with_slice = 0                 # repacks whose layout counts the slice's keys
         self.next_start = 0
         self._spare: torch.Tensor | None = None     # the other buffer of the store, after a repack
+        self._host: torch.Tensor | None = None      # pinned: the append's flags, counts and sizes
         self.verbose = os.environ.get("SEMBLO_VERBOSE", "0") == "1"
         layer.target_tokens = self.target
+
+    def _set_reserve(self, reserve: torch.Tensor, device) -> None:
+        """The reservation [Hkv, C] on the host (for the layout) and on the device (for
+        the overflow test), the latter by an asynchronous copy from pinned memory, so
+        that setting it never waits for the GPU."""
+        self.reserve = reserve
+        staged = reserve.to(torch.int32).pin_memory()
+        self._reserve_dev = staged.to(device, non_blocking=True)
 
     # -- per slice ------------------------------------------------------------------
     def slice(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
@@ -205,9 +219,20 @@ class TokenOuterPrefillSession:
             self._count_dense(timing, start, n, hq, d)
             dense_causal_attention(q, self.stage_k[:stop], self.stage_v[:stop], sm_scale=layer.scaling,
                                    chunk_start=start, out=out, timing=timing)
-        else:
-            self._append(kp, kk, vv, start, stop, store_timing)
+        elif start <= self.cap:
+            # a dense-prefix slice reads its own keys back from the store: append first
+            self._append_commit(self._append_assign(kp, start, stop, store_timing), kk, vv, store_timing)
             self._attend(q, qp, kk, vv, start, stop, out, timing)
+        else:
+            # A sparse slice reads only rows of earlier positions (the counts before it);
+            # its own keys come through the exact window.  Its attention is therefore
+            # enqueued before the append's host read, and the GPU runs it while the host
+            # waits for the flags and lays out any repack.
+            pending = self._append_assign(kp, start, stop, store_timing)
+            self.snapshot.sizes.copy_(self.index.bucket_sizes)
+            self.snapshot.chunk_start = start
+            self._attend(q, qp, kk, vv, start, stop, out, timing)
+            self._append_commit(pending, kk, vv, store_timing)
         self.next_start = stop
         return out
 
@@ -257,7 +282,7 @@ class TokenOuterPrefillSession:
         c = index.num_buckets
         width = self.tokens + c * align
         width += (-width) % PACK_ALIGN
-        self.reserve = reserved_layout(index.bucket_sizes, p, self.tokens, width, align)
+        self._set_reserve(reserved_layout(index.bucket_sizes, p, self.tokens, width, align), dev)
         indptr_h = torch.zeros(hkv, c + 1, dtype=torch.int32)
         indptr_h[:, 1:] = torch.cumsum(self.reserve, 1).to(torch.int32)
         indptr = indptr_h.to(dev)
@@ -282,20 +307,40 @@ class TokenOuterPrefillSession:
         self.stage_k = self.stage_v = self.stage_kpre = None
 
     # -- append ---------------------------------------------------------------------------
-    def _append(self, kp, kk, vv, start, stop, store_timing=None) -> None:
+    def _append_assign(self, kp, start, stop, store_timing=None):
+        """Enqueue the slice's assignment and the copy of what the host decides on:
+        overflow flags, the slice's counts and the sizes so far, into pinned memory."""
         index = self.index
-        hkv, d = kk.shape[1], kk.shape[2]
+        hkv = kp.shape[1]
         c = index.num_buckets
-        n = stop - start
-        s = _lib.stream(kk.device)
+        s = _lib.stream(kp.device)
         if store_timing is not None:
             store_timing.begin(s)
         ids = nearest_cluster(kp, index.codebooks, router_pass=True)
-        rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self.reserve)
+        rows, counts, flags = append_rows(ids, index.bucket_indptr, index.bucket_sizes, self._reserve_dev)
         if store_timing is not None:
             store_timing.end(s)
-        # the one host read per slice: flags, the slice's counts and the sizes so far
-        host = torch.cat([flags, counts.flatten(), index.bucket_sizes.flatten()]).cpu()
+        words = hkv + 2 * hkv * c
+        if self._host is None or self._host.numel() != words:
+            self._host = torch.empty(words, dtype=torch.int32, pin_memory=True)
+        self._host.copy_(torch.cat([flags, counts.flatten(), index.bucket_sizes.flatten()]),
+                         non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(kp.device))
+        return dict(ids=ids, rows=rows, counts=counts, ready=ready, start=int(start), stop=int(stop))
+
+    def _append_commit(self, pending, kk, vv, store_timing=None) -> None:
+        """The append's one host read per slice, any repack it decides, and the K/V
+        writes (token_outer_prefill.py:339-364)."""
+        index = self.index
+        hkv, d = kk.shape[1], kk.shape[2]
+        c = index.num_buckets
+        start, stop = pending["start"], pending["stop"]
+        n = stop - start
+        s = _lib.stream(kk.device)
+        ids, rows, counts = pending["ids"], pending["rows"], pending["counts"]
+        pending["ready"].synchronize()
+        host = self._host
         flags_h = host[:hkv]
         if bool((flags_h & 2).any()):
             raise RuntimeError("a key was assigned outside the cluster range")
@@ -343,9 +388,9 @@ class TokenOuterPrefillSession:
         packed = index.packed_kv
         hkv, width, d = packed.shape[2], packed.shape[1], packed.shape[3]
         c = index.num_buckets
-        new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32)
+        new_ip = torch.zeros(hkv, c + 1, dtype=torch.int32, pin_memory=True)
         new_ip[:, 1:] = torch.cumsum(reserve, 1).to(torch.int32)
-        new_ip = new_ip.to(packed.device)
+        new_ip = new_ip.to(packed.device, non_blocking=True)
         if self._spare is None:
             self._spare = torch.zeros_like(packed)
         dst = self._spare
@@ -357,7 +402,7 @@ class TokenOuterPrefillSession:
                   _lib.stream(packed.device))
         index.packed_kv, self._spare = dst, packed
         index.bucket_indptr.copy_(new_ip)                             # same address as before
-        self.reserve = reserve
+        self._set_reserve(reserve, packed.device)
         index.extras["reserve"] = reserve
         self.repacks += 1
         if self.verbose:

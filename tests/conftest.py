@@ -13,3 +13,4 @@ for p in (str(ROOT), str(PKG_DIR), str(ROOT / "tests" / "golden")):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")
+    config.addinivalue_line("markers", "emu: runs the HIP kernels on the CPU through tests/emu (slow)")

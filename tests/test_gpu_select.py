@@ -24,7 +24,7 @@ def _select_gpu(vectors, codebooks, sizes, *, tau, beta, target, g_union, logmix
     from semblo_amd.fused_select import theta_select_bitmask_flat
     q, hq, d = vectors.shape
     hkv, _, c, _ = codebooks.shape
-    nb = sizes.shape[0]
+    nb = max(sizes.shape[0], (q + g_union - 1) // g_union)    # one bitmask row per query block
     bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=DEV)
     qmask = torch.zeros(q, hkv, c // 32, dtype=torch.int32, device=DEV)
     prob = torch.empty(q, hkv, c, dtype=torch.float32, device=DEV)
