@@ -438,11 +438,21 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
         attn_ms = timed.total_ms() / max(steps, 1)
         flops = timing.total_flops()
         achieved = flops / (attn_ms * 1e-3) / 1e12
+        by_form = {}
+        for kind in ("dense", "sparse"):
+            ms_k, n_k = timed.split(kind, steps)
+            fl_k = timing.split_flops(kind)
+            if n_k and ms_k > 0:
+                ach = fl_k / (ms_k * 1e-3) / 1e12
+                by_form[kind] = {"launches": n_k, "ms": round(ms_k, 3), "tflop": round(fl_k / 1e12, 3),
+                                 "achieved": round(ach, 1), "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
         result.update(prefill_ms=ms, attn_ms=attn_ms, flops=flops, achieved=achieved,
-                      launches=timing.launches())
+                      launches=timing.launches(), by_form=by_form)
         assert timed.launches() == timing.launches() * max(steps, 1)
         _log(f"attention kernel {attn_ms:.2f} ms over {timing.launches()} launches, "
-             f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s")
+             f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s ("
+             + ", ".join(f"{k} chunks {v['ms']:.2f} ms, {v['achieved']:.0f} TFLOP/s" for k, v in by_form.items())
+             + ")")
         if store is not None:
             st_ms = store.total_ms()
             st_bytes = store.total_flops()           # the store timing collects bytes
@@ -502,7 +512,8 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
             "traffic": measured_traffic(config),
             "kernel": "attn_items_kernel<256,4,*> (dense chunks: compact form, sparse chunks: pipelined form)",
             "flops_per_layer": result["flops"], "kernel_ms_per_layer": round(result["attn_ms"], 3),
-            "launches_per_layer": result["launches"]},
+            "launches_per_layer": result["launches"],
+            "by_form": result.get("by_form")},
         "decode_roofline": None if "decode_us" not in result else {
             "bound": "hbm", "achieved": round(result["decode_gbs"], 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(result["decode_gbs"] / PEAK_HBM_GBS, 4),

@@ -57,12 +57,18 @@ int sbsa_kmeans_assign(const void* x_bf16, int64_t ld_x, const int32_t* row_inde
                        const void* cent_bf16, int num_clusters, int dim, int32_t* assign,
                        hipStream_t stream);
 
-/* Deterministic per-cluster fp32 sums and counts of the sample rows: replaces
- * _segment_sum / torch.bincount in fit_flat_codebook
- * (semblo/inference/flat_index.py:87-141, 268-272).  sums [C, dim], counts [C]. */
+/* Deterministic per-cluster fp32 sums and counts of the sample rows (the sum
+ * order depends on the assignment only): replaces _segment_sum / torch.bincount
+ * in fit_flat_codebook (semblo/inference/flat_index.py:87-141, 268-272).
+ * sums [C, dim], counts [C]; C <= 1024; dim and ld_x multiples of 4 and x
+ * 16-byte aligned (SBSA_ERR_UNSUPPORTED otherwise).  member_bits is device scratch of at
+ * least sbsa_kmeans_member_bits_bytes(n, C) bytes, 16-byte aligned (one bitmap
+ * of the rows per cluster; overwritten, need not be cleared). */
+size_t sbsa_kmeans_member_bits_bytes(int64_t n, int num_clusters);
 int sbsa_kmeans_update(const float* x, int64_t ld_x, const int32_t* row_index, int64_t n,
                        const int32_t* assign, int num_clusters, int dim, float* sums,
-                       int32_t* counts, hipStream_t stream);
+                       int32_t* counts, uint32_t* member_bits, size_t member_bits_bytes,
+                       hipStream_t stream);
 
 /* Centroid step of fit_flat_codebook (semblo/inference/flat_index.py:255-289)
  * and the descriptor of _build_flat (semblo/vllm_plugin/state.py:877-886).
@@ -77,16 +83,29 @@ int sbsa_kmeans_centroids(int mode, const float* sums, const int32_t* counts,
                           void* cent_bf16, hipStream_t stream);
 
 /* Iterations it0 .. it1-1 of fit_flat_codebook's k-means loop
- * (semblo/inference/flat_index.py:264-289) without restarts, in one call:
- * each is sbsa_kmeans_assign, sbsa_kmeans_update into sums_hist[it] [C, dim]
- * and counts_hist[it] [C], and sbsa_kmeans_centroids mode 1 with no_restart
- * (C entries of -1).  The rows are x (bf16 for the assignment, fp32 for the
- * sums, both with row stride ld_x) at row_index [n]; assign [n] is scratch. */
+ * (semblo/inference/flat_index.py:264-289) in one call: each is
+ * sbsa_kmeans_assign, sbsa_kmeans_update into sums_hist[it] [C, dim] and
+ * counts_hist[it] [C], and the centroid step.  The rows are x (bf16 for the
+ * assignment, fp32 for the sums, both with row stride ld_x) at row_index [n];
+ * assign [n] and member_bits (as for sbsa_kmeans_update) are scratch.
+ *   restart_rows null: no restarts (sbsa_kmeans_centroids mode 1 with
+ *     no_restart, C entries of -1); an iteration that leaves a cluster empty
+ *     is for the caller to find in counts_hist and redo.
+ *   restart_rows [restart_draws, C]: the k-th iteration that leaves clusters
+ *     empty (k < restart_draws) restarts them on sample rows restart_rows[k][0..],
+ *     in cluster order -- the k-th restart draw the reference makes
+ *     (flat_index.py:277-283), made ahead by the caller.  restart_flags
+ *     [it1 + 1]: restart_flags[it0] must hold the number of iterations before
+ *     it0 that left a cluster empty (0 for it0 = 0); iteration it writes
+ *     restart_flags[it + 1].  Later empty iterations are not restarted: the
+ *     caller finds them in counts_hist and redoes them. */
 int sbsa_kmeans_iterate(const void* x_bf16, const float* x_f32, int64_t ld_x,
                         const int32_t* row_index, int64_t n, int num_clusters, int dim,
                         int32_t* assign, float* sums_hist, int32_t* counts_hist,
-                        const int32_t* no_restart, float* cent_f32, void* cent_bf16, int it0,
-                        int it1, hipStream_t stream);
+                        const int32_t* no_restart, const int32_t* restart_rows,
+                        int restart_draws, int32_t* restart_flags, float* cent_f32,
+                        void* cent_bf16, uint32_t* member_bits, size_t member_bits_bytes,
+                        int it0, int it1, hipStream_t stream);
 
 /* Stable counting sort of positions by cluster into page-aligned runs:
  * replaces argsort/bincount + _page_align_order

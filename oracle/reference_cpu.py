@@ -31,7 +31,9 @@ Parity pins (each checked by a test in tests/):
   S0   closed form: unit norm of the bf16 result; reproduces the reference's
        torch fallback op for op.
   S1   golden vectors written by the reference's own ``ProductPostingIndex.build``
-       on CPU (tests/golden/make_golden.py) -- bit-exact.
+       on CPU (tests/golden/make_golden.py) -- bit-exact, with and without an
+       attention sink (SEMBLO_SINK_TOKENS); the sink's hold-out and forced bit by
+       the known answers of the reference's tests/test_fitted_sink.py:100-117.
   S2   fp64 loop form of the score (tests/test_oracle.py).
   S3   golden vectors of the reference's Triton select kernel run under the
        Triton CPU interpreter, plus the sorted-rule bound (sorted set is a subset
@@ -201,12 +203,20 @@ def page_align_order(order: torch.Tensor, counts: torch.Tensor, positions: torch
     return new_order, ip_pad.to(torch.int32), inverse
 
 
+def check_sink_partition(sink: int, length: int, fit_length: int, num_clusters: int) -> None:
+    """state.py:26-34: the sink settings the paper path refuses."""
+    if sink % 16:
+        raise RuntimeError(f"SEMBLO_SINK_TOKENS={sink}: a multiple of 16 keeps the sink cluster page-aligned")
+    if length <= sink or fit_length - sink < 2 * num_clusters:
+        raise RuntimeError(f"SEMBLO_SINK_TOKENS={sink} leaves too few keys")
+
+
 def build_flat_index(product_keys: torch.Tensor, positions: torch.Tensor | None = None, *,
                      unit_tokens: int = 2048, min_clusters_log2: int = 7,
                      sample_size: int = 8192, fit_iters: int = 8, per_centroid: int = 32,
                      codebook_seed: int = 0, page_align: int = 16,
                      num_clusters: int | None = None, traces: list | None = None,
-                     fit_steps: list | None = None) -> dict:
+                     fit_steps: list | None = None, sink_tokens: int = 0) -> dict:
     """ProductPostingIndex._build_flat, state.py:545-948, on the paper path.
 
     product_keys [L, Hkv, I] are the router's output (routing_normalize_keys of
@@ -214,6 +224,11 @@ def build_flat_index(product_keys: torch.Tensor, positions: torch.Tensor | None 
     ``codebook_seed`` (state.py:520-523), used for every head in turn.
     Returns codebooks [Hkv, 2, C, I/2] (key dtype), posting [Hkv, W] int32,
     indptr [Hkv, C+1] int32, sizes [Hkv, C] int32, inverse [Hkv, L] int32.
+
+    ``sink_tokens`` S > 0 (SEMBLO_SINK_TOKENS, state.py:757-782): positions 0..S-1
+    form cluster 0 with a zero centroid; positions S.. are fitted into C-1
+    clusters (sample min(fit_sample, L-S)) and assigned to them as ids 1..C-1.
+    ``fit_steps`` then describes that fit (rows S..).
     """
     length, num_kv_heads, index_dim = product_keys.shape
     if positions is None:
@@ -222,19 +237,32 @@ def build_flat_index(product_keys: torch.Tensor, positions: torch.Tensor | None 
     gen.manual_seed(int(codebook_seed))
     c = num_clusters or num_flat_clusters(length, unit_tokens, min_clusters_log2)
     codebooks, posting_rows, indptr_rows, size_rows, inverse_rows = [], [], [], [], []
+    sink = int(sink_tokens)
+    if sink:
+        check_sink_partition(sink, length, length, c)
     for h in range(num_kv_heads):
         keys = product_keys[:, h]
         space = routing_space(keys)
         fit_sample = min(length, max(int(sample_size), per_centroid * c))
         trace = [] if traces is not None else None
         steps = [] if fit_steps is not None else None
-        cents = fit_flat_codebook(space, c, num_iters=fit_iters, sample_size=fit_sample,
-                                  generator=gen, trace=trace, steps=steps)
+        if sink:
+            rest = fit_flat_codebook(space[sink:], c - 1, num_iters=fit_iters,
+                                     sample_size=min(fit_sample, length - sink), generator=gen,
+                                     trace=trace, steps=steps)
+            cents = torch.cat([rest.new_zeros(1, rest.shape[1]), rest], dim=0)
+            rest_assign = argmax_sim_chunked(F.normalize(space[sink:].float(), dim=-1), rest, 65536)
+            assign = torch.cat([torch.zeros(sink, dtype=torch.long), rest_assign.long() + 1])
+            fit_cents, fit_assign = rest, rest_assign
+        else:
+            cents = fit_flat_codebook(space, c, num_iters=fit_iters, sample_size=fit_sample,
+                                      generator=gen, trace=trace, steps=steps)
+            assign = argmax_sim_chunked(F.normalize(space.float(), dim=-1), cents, 65536)
+            fit_cents, fit_assign = cents, assign
         if traces is not None:
             traces.append(trace)
-        assign = argmax_sim_chunked(F.normalize(space.float(), dim=-1), cents, 65536)
         if fit_steps is not None:
-            fit_steps.append(dict(steps=steps, final_centroids=cents, final_assign=assign))
+            fit_steps.append(dict(steps=steps, final_centroids=fit_cents, final_assign=fit_assign))
         order = torch.argsort(assign, stable=True)
         counts = torch.bincount(assign, minlength=c).to(torch.int32)
         if page_align > 1:
@@ -372,6 +400,21 @@ def theta_select(prob: torch.Tensor, sizes: torch.Tensor, *, beta: float, target
             union[b] = rows.any(dim=0)
     return dict(sel=sel, theta=theta, score=score, counts=counts, tokens=tokens,
                 bitmask=pack_bits(union), qmask=pack_bits(sel), all_fit=all_fit)
+
+
+def hold_out_sink(sizes: torch.Tensor, target_tokens: int, sink: int):
+    """fused_prefill.py:202-209: the selector's sizes with cluster 0 hidden (a copy), and
+    the budget the other clusters share."""
+    held = sizes.clone()
+    held[..., 0] = 0
+    return held, max(0, int(target_tokens) - int(sink))
+
+
+def force_sink_bit(*masks) -> None:
+    """fused_prefill.py:212-216: cluster 0 selected in every row of every mask, in place."""
+    for m in masks:
+        if m is not None:
+            m[..., 0].bitwise_or_(1)
 
 
 def sorted_select(score: torch.Tensor, sizes: torch.Tensor, target_tokens: float,

@@ -197,78 +197,148 @@ __global__ __launch_bounds__(256) void kmeans_assign_kernel(
     }
 }
 
-// Per-cluster fp32 sums of the member rows, in row order (deterministic).
-// One block per cluster takes the assignment in chunks of 4096 rows: each
-// wave compacts the members of its 1024 contiguous rows into its own list
-// (ballots, no block barrier), the four lists form the chunk's members in row
-// order, and each thread adds its dimensions of those rows in that order with
-// eight rows' loads in flight.
-constexpr int KU_CHUNK = 4096;
+// Per-cluster fp32 sums of the member rows, in row order (deterministic), in
+// two launches whose traffic grows with the rows, not with rows x clusters.
+//
+// kmeans_members_kernel writes one bitmap row per cluster: bit i of bits[c] is
+// set iff assign[i] == c.  A block takes 512 rows (16 words of 32 bits), ORs
+// their bits into an LDS table [C][16] (the OR commutes, so the result does not
+// depend on the order of the LDS atomics) and writes the whole table out, zero
+// words included, as 64-byte pieces of each cluster's row: no state is kept
+// from call to call.  Words per cluster W = ceil(n / 512) * 16.
+constexpr int KB_ROWS = 512;
+constexpr int KB_WORDS = KB_ROWS / 32;
 
+__global__ __launch_bounds__(256) void kmeans_members_kernel(const int32_t* __restrict__ assign,
+                                                              int64_t n, int num_clusters,
+                                                              int64_t words, uint32_t* __restrict__ bits) {
+  extern __shared__ u32x4_t tab4[];          // [C][16] words as [C][4] 16-byte pieces
+  uint32_t* tab = reinterpret_cast<uint32_t*>(tab4);
+  const int64_t r0 = (int64_t)blockIdx.x * KB_ROWS;
+  int a[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int64_t i = r0 + threadIdx.x + 256 * k;
+    a[k] = i < n ? assign[i] : -1;
+  }
+  for (int i = threadIdx.x; i < num_clusters * 4; i += 256) tab4[i] = u32x4_t{0u, 0u, 0u, 0u};
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int local = threadIdx.x + 256 * k;
+    if ((unsigned)a[k] < (unsigned)num_clusters)
+      atomicOr(&tab[a[k] * KB_WORDS + (local >> 5)], 1u << (local & 31));
+  }
+  __syncthreads();
+  u32x4_t* out = reinterpret_cast<u32x4_t*>(bits);
+  for (int i = threadIdx.x; i < num_clusters * 4; i += 256) {
+    const int c = i >> 2, q = i & 3;
+    out[((int64_t)c * words + (int64_t)blockIdx.x * KB_WORDS) / 4 + q] = tab4[i];
+  }
+}
+
+// kmeans_update_kernel: one block per cluster reads its bitmap row, 4 words a
+// thread per segment of 1024 words (32768 rows).  A block-wide prefix sum of the
+// threads' bit counts places each member at its rank in an LDS list, so the list
+// holds the cluster's rows in row order; the list is mapped through the row map
+// in one pass.  Wave w then adds list entries w, w+4, w+8, ... (4 dims a lane,
+// 16-byte loads), the loads of KU_BATCH entries issued before any of them is
+// added, so one round trip covers 4 * KU_BATCH rows.  A segment with more members
+// than the list holds is taken in windows.  The four waves' sums are added in
+// wave order at the end: the result depends on the assignment only.
+constexpr int KU_LIST = 8192;
+constexpr int KU_SEG = 1024;     // words per segment, 4 a thread
+constexpr int KU_BATCH = 16;     // entries per wave per round trip
+
+template <int NJ>  // dims 4*lane + 256*j .. +3 for j < NJ
 __global__ __launch_bounds__(256) void kmeans_update_kernel(
-    const float* __restrict__ x, int64_t ld_x, const int32_t* __restrict__ row_index, int64_t n,
-    const int32_t* __restrict__ assign, int dim, float* __restrict__ sums,
+    const float* __restrict__ x, int64_t ld_x, const int32_t* __restrict__ row_index,
+    const uint32_t* __restrict__ bits, int64_t words, int dim, float* __restrict__ sums,
     int32_t* __restrict__ counts) {
-  __shared__ int members[KU_CHUNK];        // source rows, wave w's at [w * 1024, ...)
-  __shared__ int wave_cnt[4];
+  __shared__ int members[KU_LIST];
+  __shared__ __attribute__((aligned(16))) float red[4][256 * NJ];
+  __shared__ int wsum[4];
   const int c = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const uint64_t below = (1ull << lane) - 1;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims threadIdx.x + 256*j, dim <= 1024
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const uint32_t* row = bits + (int64_t)c * words;
+  f32x4_t acc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   int total = 0;
-  for (int64_t base = 0; base < n; base += KU_CHUNK) {
-    const int64_t seg = base + wave * (KU_CHUNK / 4);
-    int cnt_w = 0;
-#pragma unroll 4
-    for (int k = 0; k < KU_CHUNK / 4 / 64; ++k) {
-      const int64_t i = seg + k * 64 + lane;
-      const bool mine = i < n && assign[i] == c;
-      const uint64_t ball = __ballot(mine);
-      if (mine) members[wave * (KU_CHUNK / 4) + cnt_w + __popcll(ball & below)] =
-          row_index ? row_index[i] : (int)i;
-      cnt_w += __popcll(ball);
+  for (int64_t w0 = 0; w0 < words; w0 += KU_SEG) {
+    u32x4_t q = {0u, 0u, 0u, 0u};
+    const int64_t w = w0 + 4 * t;
+    if (w < words) q = *reinterpret_cast<const u32x4_t*>(row + w);   // words is a multiple of 16
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const int cnt = __builtin_popcount(q.x) + __builtin_popcount(q.y) + __builtin_popcount(q.z) +
+                    __builtin_popcount(q.w);
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
     }
-    if (lane == 0) wave_cnt[wave] = cnt_w;
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    for (int w = 0; w < 4; ++w) {
-      const int* lst = members + w * (KU_CHUNK / 4);
-      const int cnt = wave_cnt[w];
-      int m = 0;
-      for (; m + 8 <= cnt; m += 8) {
-        float v[8][4];
+    int excl = incl - cnt;
+    for (int v = 0; v < wave; ++v) excl += wsum[v];
+    const int seg_total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    for (int lo = 0; lo < seg_total; lo += KU_LIST) {
+      if (excl < lo + KU_LIST && excl + cnt > lo) {
+        int pos = excl;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int64_t src = lst[m + u];
+        for (int k = 0; k < 4; ++k) {
+          uint32_t m = qw[k];
+          while (m) {
+            const int bit = __builtin_ctz(m);
+            m &= m - 1;
+            if (pos >= lo && pos < lo + KU_LIST) members[pos - lo] = (int)((w + k) * 32 + bit);
+            ++pos;
+          }
+        }
+      }
+      __syncthreads();
+      const int listed = min(KU_LIST, seg_total - lo);
+      if (row_index) {
+        for (int i = t; i < listed; i += 256) members[i] = row_index[members[i]];
+        __syncthreads();
+      }
+      for (int m = wave; m < listed; m += 4 * KU_BATCH) {
+        f32x4_t v[KU_BATCH][NJ];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int d = threadIdx.x + 256 * j;
-            v[u][j] = d < dim ? x[src * ld_x + d] : 0.f;
+        for (int u = 0; u < KU_BATCH; ++u) {
+          const bool ok = m + 4 * u < listed;
+          const int64_t src = ok ? members[m + 4 * u] : 0;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int d = 4 * lane + 256 * j;
+            v[u][j] = (ok && d < dim) ? *reinterpret_cast<const f32x4_t*>(x + src * ld_x + d)
+                                      : f32x4_t{0.f, 0.f, 0.f, 0.f};
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < KU_BATCH; ++u)
+          if (m + 4 * u < listed)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[j] += v[u][j];
+            for (int j = 0; j < NJ; ++j) acc[j] += v[u][j];
       }
-      for (; m < cnt; ++m) {
-        const int64_t src = lst[m];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = threadIdx.x + 256 * j;
-          if (d < dim) acc[j] += x[src * ld_x + d];
-        }
-      }
-      total += cnt;
+      __syncthreads();  // the list is free for the next window
     }
-    __syncthreads();
+    total += seg_total;
+    __syncthreads();    // wsum may be rewritten
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int d = threadIdx.x + 256 * j;
-    if (d < dim) sums[(int64_t)c * dim + d] = acc[j];
+  for (int j = 0; j < NJ; ++j)
+    *reinterpret_cast<f32x4_t*>(&red[wave][4 * lane + 256 * j]) = acc[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int d = t + 256 * j;
+    if (d < dim) sums[(int64_t)c * dim + d] = ((red[0][d] + red[1][d]) + red[2][d]) + red[3][d];
   }
-  if (threadIdx.x == 0) counts[c] = total;
+  if (t == 0) counts[c] = total;
 }
 
 // Centroid step, one wave per cluster.
@@ -276,20 +346,47 @@ __global__ __launch_bounds__(256) void kmeans_update_kernel(
 //  mode 1 (update):     cent = normalize(sums / counts), an empty cluster
 //                       (src[c] >= 0) restarts on sample row src[c]  flat_index.py:277-288
 //  mode 2 (descriptor): out = bf16(normalize(sums)) as [2, C, dim/2] state.py:883-886
+//  mode 3 (update with restarts drawn ahead): mode 1, where the empty clusters
+//                       of the k-th iteration that has any (k < draws) restart
+//                       on the sample rows src[k * C + rank], rank counting the
+//                       empty clusters in cluster order (src holds the restart
+//                       draws, made ahead).  flags[0] = k, the number of earlier
+//                       iterations with an empty cluster; block 0 writes
+//                       flags[1] = k + (this iteration has one), for the next
+//                       iteration's launch.
 __global__ void kmeans_centroids_kernel(int mode, const float* __restrict__ sums,
                                         const int32_t* __restrict__ counts,
                                         const int32_t* __restrict__ src,
                                         const float* __restrict__ x, int64_t ld_x,
                                         const int32_t* __restrict__ row_index, int num_clusters,
                                         int dim, float* __restrict__ cent_f32,
-                                        bf16_t* __restrict__ cent_bf16) {
+                                        bf16_t* __restrict__ cent_bf16, int32_t* flags,
+                                        int draws) {
   const int lane = threadIdx.x & 63;
   const int c = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const bool update = mode == 1 || mode == 3;
+  int used = 0;
+  if (mode == 3) {
+    used = flags[0];
+    if (blockIdx.x == 0 && threadIdx.x < 64) {
+      int any = 0;
+      for (int i = lane; i < num_clusters; i += 64) any |= counts[i] == 0;
+      any = __ballot(any) != 0ull;
+      if (lane == 0) flags[1] = used + any;
+    }
+  }
   if (c >= num_clusters) return;
   const int per = (dim + 63) / 64;
   float v[16];
-  if (mode == 0 || (mode == 1 && src[c] >= 0)) {
-    int64_t r = src[c];
+  int64_t r = -1;
+  if (mode == 0 || mode == 1) {
+    r = src[c];
+  } else if (mode == 3 && used < draws && counts[c] == 0) {
+    int rank = 0;
+    for (int b = 0; b < c; b += 64) rank += __popcll(__ballot(b + lane < c && counts[b + lane] == 0));
+    r = src[(int64_t)used * num_clusters + rank];
+  }
+  if (r >= 0) {
     int64_t srow = row_index ? (int64_t)row_index[r] : r;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -297,12 +394,12 @@ __global__ void kmeans_centroids_kernel(int mode, const float* __restrict__ sums
       v[i] = (i < per && d < dim) ? x[srow * ld_x + d] : 0.f;
     }
   } else {
-    float cnt = (mode == 1) ? (float)counts[c] : 1.0f;
+    float cnt = update ? (float)counts[c] : 1.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       int d = lane + 64 * i;
       float s = (i < per && d < dim) ? sums[(int64_t)c * dim + d] : 0.f;
-      v[i] = (mode == 1) ? s / cnt : s;
+      v[i] = update ? s / cnt : s;
     }
   }
   if (mode != 0) {
@@ -660,13 +757,32 @@ int sbsa_kmeans_assign(const void* x_bf16, int64_t ld_x, const int32_t* row_inde
   return SBSA_OK;
 }
 
+size_t sbsa_kmeans_member_bits_bytes(int64_t n, int num_clusters) {
+  if (n < 0 || num_clusters < 1) return 0;
+  const int64_t words = (n + KB_ROWS - 1) / KB_ROWS * KB_WORDS;
+  return (size_t)(words * num_clusters) * sizeof(uint32_t);
+}
+
 int sbsa_kmeans_update(const float* x, int64_t ld_x, const int32_t* row_index, int64_t n,
                        const int32_t* assign, int num_clusters, int dim, float* sums,
-                       int32_t* counts, hipStream_t stream) {
-  if (!x || !assign || !sums || !counts || n < 0 || num_clusters < 1) return SBSA_ERR_ARG;
-  if (dim < 1 || dim > 1024) return SBSA_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kmeans_update_kernel, dim3(num_clusters), dim3(256), 0, stream, x, ld_x,
-                     row_index, n, assign, dim, sums, counts);
+                       int32_t* counts, uint32_t* member_bits, size_t member_bits_bytes,
+                       hipStream_t stream) {
+  if (!x || !assign || !sums || !counts || !member_bits || n < 0 || num_clusters < 1)
+    return SBSA_ERR_ARG;
+  if (dim < 4 || dim > 1024 || dim % 4 || ld_x % 4 || ((uintptr_t)x & 15) || num_clusters > 1024)
+    return SBSA_ERR_UNSUPPORTED;
+  if (member_bits_bytes < sbsa_kmeans_member_bits_bytes(n, num_clusters)) return SBSA_ERR_CAPACITY;
+  if (((uintptr_t)member_bits & 15) != 0) return SBSA_ERR_ARG;
+  const int64_t words = (n + KB_ROWS - 1) / KB_ROWS * KB_WORDS;
+  if (words > 0)
+    hipLaunchKernelGGL(kmeans_members_kernel, dim3((unsigned)(words / KB_WORDS)), dim3(256),
+                       (size_t)num_clusters * KB_WORDS * sizeof(uint32_t), stream, assign, n,
+                       num_clusters, words, member_bits);
+  auto kernel = dim <= 256 ? kmeans_update_kernel<1>
+                : dim <= 512 ? kmeans_update_kernel<2>
+                : dim <= 768 ? kmeans_update_kernel<3> : kmeans_update_kernel<4>;
+  hipLaunchKernelGGL(kernel, dim3(num_clusters), dim3(256), 0, stream, x, ld_x, row_index,
+                     (const uint32_t*)member_bits, words, dim, sums, counts);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }
@@ -682,7 +798,7 @@ int sbsa_kmeans_centroids(int mode, const float* sums, const int32_t* counts,
   if (mode == 2 && !sums) return SBSA_ERR_ARG;
   hipLaunchKernelGGL(kmeans_centroids_kernel, dim3((num_clusters + 3) / 4), dim3(256), 0, stream,
                      mode, sums, counts, src_rows, x, ld_x, row_index, num_clusters, dim, cent_f32,
-                     (bf16_t*)cent_bf16);
+                     (bf16_t*)cent_bf16, (int32_t*)nullptr, 0);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }
@@ -690,18 +806,30 @@ int sbsa_kmeans_centroids(int mode, const float* sums, const int32_t* counts,
 int sbsa_kmeans_iterate(const void* x_bf16, const float* x_f32, int64_t ld_x,
                         const int32_t* row_index, int64_t n, int num_clusters, int dim,
                         int32_t* assign, float* sums_hist, int32_t* counts_hist,
-                        const int32_t* no_restart, float* cent_f32, void* cent_bf16, int it0,
-                        int it1, hipStream_t stream) {
-  if (!sums_hist || !counts_hist || !no_restart || it0 < 0 || it1 < it0) return SBSA_ERR_ARG;
+                        const int32_t* no_restart, const int32_t* restart_rows,
+                        int restart_draws, int32_t* restart_flags, float* cent_f32,
+                        void* cent_bf16, uint32_t* member_bits, size_t member_bits_bytes,
+                        int it0, int it1, hipStream_t stream) {
+  if (!sums_hist || !counts_hist || it0 < 0 || it1 < it0) return SBSA_ERR_ARG;
+  if (restart_rows ? (!restart_flags || restart_draws < 1) : !no_restart) return SBSA_ERR_ARG;
   for (int it = it0; it < it1; ++it) {
     float* sums = sums_hist + (int64_t)it * num_clusters * dim;
     int32_t* counts = counts_hist + (int64_t)it * num_clusters;
     int rc = sbsa_kmeans_assign(x_bf16, ld_x, row_index, n, cent_bf16, num_clusters, dim, assign, stream);
     if (rc == SBSA_OK)
-      rc = sbsa_kmeans_update(x_f32, ld_x, row_index, n, assign, num_clusters, dim, sums, counts, stream);
-    if (rc == SBSA_OK)
+      rc = sbsa_kmeans_update(x_f32, ld_x, row_index, n, assign, num_clusters, dim, sums, counts,
+                              member_bits, member_bits_bytes, stream);
+    if (rc == SBSA_OK && !restart_rows)
       rc = sbsa_kmeans_centroids(1, sums, counts, no_restart, x_f32, ld_x, row_index, num_clusters,
                                  dim, cent_f32, cent_bf16, stream);
+    if (rc == SBSA_OK && restart_rows) {
+      if (!cent_f32 || !cent_bf16 || dim < 2 || dim > 1024 || dim % 2) return SBSA_ERR_ARG;
+      hipLaunchKernelGGL(kmeans_centroids_kernel, dim3((num_clusters + 3) / 4), dim3(256), 0,
+                         stream, 3, sums, counts, restart_rows, x_f32, ld_x, row_index,
+                         num_clusters, dim, cent_f32, (bf16_t*)cent_bf16, restart_flags + it,
+                         restart_draws);
+      SBSA_CHECK_LAUNCH();
+    }
     if (rc != SBSA_OK) return rc;
   }
   return SBSA_OK;

@@ -26,8 +26,10 @@ SIGNATURES = {
     "sbsa_route_vectors": (I32, [P, I64, I64, I32, I32, P, I64, P]),
     "sbsa_key_space": (I32, [P, I64, I64, I32, I32, P, P, P]),
     "sbsa_kmeans_assign": (I32, [P, I64, P, I64, P, I32, I32, P, P]),
-    "sbsa_kmeans_update": (I32, [P, I64, P, I64, P, I32, I32, P, P, P]),
-    "sbsa_kmeans_iterate": (I32, [P, P, I64, P, I64, I32, I32, P, P, P, P, P, P, I32, I32, P]),
+    "sbsa_kmeans_update": (I32, [P, I64, P, I64, P, I32, I32, P, P, P, SZ, P]),
+    "sbsa_kmeans_member_bits_bytes": (SZ, [I64, I32]),
+    "sbsa_kmeans_iterate": (I32, [P, P, I64, P, I64, I32, I32, P, P, P, P, P, I32, P, P, P, P, SZ,
+                                     I32, I32, P]),
     "sbsa_kmeans_centroids": (I32, [I32, P, P, P, P, I64, P, I32, I32, P, P, P]),
     "sbsa_bucket_layout_workspace_bytes": (SZ, [I64, I32]),
     "sbsa_bucket_layout": (I32, [P, I64, I32, I32, P, P, P, I64, P, P, P, SZ, P]),

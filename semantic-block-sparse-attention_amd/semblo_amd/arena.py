@@ -45,6 +45,7 @@ class DecodeArena:
         table[base:last + 1] = phys
         self.suffix_table = table.to(dev)
         self.prompt_length_t = torch.tensor([self.prompt_length], dtype=torch.int32, device=dev)
+        self.steps = 0          # decode steps taken through the layer (host count, no device read)
 
     def suffix_rows(self, positions: torch.Tensor, kv_head: int):
         """K and V of the generated tokens at ``positions`` (host helper for tests)."""

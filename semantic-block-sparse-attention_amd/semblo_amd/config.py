@@ -6,6 +6,7 @@ power-of-two cluster count).
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 PAGE = 16                    # SEMBLO_FA3_BODY / SEMBLO_FA3_ALIGN
@@ -19,6 +20,23 @@ def flat_cluster_count(length: int, target_size: int, *, min_clusters: int = 64,
                        max_clusters: int = 16384) -> int:
     """flat_index.py:81-84."""
     return int(min(max(length // max(target_size, 1), min_clusters), max_clusters, length))
+
+
+def fitted_sink_tokens() -> int:
+    """SEMBLO_SINK_TOKENS (default 0, off): with S > 0 the fitted partition reserves
+    cluster 0 for positions 0..S-1, its descriptor zero, and every selection takes it
+    first inside a budget reduced by S (state.py:21-23, fused_prefill.py:192-216)."""
+    return max(0, int(os.environ.get("SEMBLO_SINK_TOKENS", "0") or "0"))
+
+
+def check_sink_partition(sink: int, length: int, fit_length: int, num_clusters: int) -> None:
+    """The settings a reserved sink cluster does not compose with (state.py:26-34, the
+    checks that apply to this build's partition)."""
+    if sink % 16:
+        raise RuntimeError(f"SEMBLO_SINK_TOKENS={sink}: a multiple of 16 keeps the sink cluster page-aligned")
+    if length <= sink or fit_length - sink < 2 * num_clusters:
+        raise RuntimeError(f"SEMBLO_SINK_TOKENS={sink} leaves too few keys ({length:,} in the prompt, "
+                           f"{fit_length:,} to fit) for {num_clusters - 1} clusters")
 
 
 def num_flat_clusters(length: int, unit_tokens: int = FLAT_UNIT_TOKENS,

@@ -13,6 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .config import fitted_sink_tokens
 from .fused_prefill import PagedSparseAttentionResult
 
 
@@ -80,7 +81,8 @@ def fused_decode_step(layer, arena, *, q_post: torch.Tensor, q_pre: torch.Tensor
             _lib.ptr(arena.packed_kv), arena.packed_kv.shape[1], _lib.ptr(arena.suffix_kv),
             arena.suffix_kv.shape[1], arena.suffix_block, _lib.ptr(arena.suffix_table),
             arena.prompt_length, arena.max_tiles, hq, hkv, c, d, 1.0 / float(temperature),
-            float(beta), float(target_tokens), int(iters), 0, float(sm_scale), int(num_splits), ss)
+            float(beta), float(target_tokens), int(iters), fitted_sink_tokens(), float(sm_scale),
+            int(num_splits), ss)
     tail = (_lib.ptr(out), out.stride(0), _lib.ptr(out_lse), _lib.ptr(csr_out), _lib.stream(q.device))
     if no_alloc:
         _lib.call("sbsa_decode_step_noalloc", *head, *tail)
@@ -130,6 +132,7 @@ def decode_prompt_only(q_chunk: torch.Tensor, vectors: torch.Tensor, index, *, t
               _lib.ptr(holder.packed_kv), holder.packed_kv.shape[1], _lib.ptr(holder.suffix_kv), 1,
               256, _lib.ptr(holder.suffix_table), holder.prompt_length, holder.max_tiles, hq, hkv,
               index.num_buckets, d, 1.0 / float(temperature), float(beta), float(target_tokens),
-              int(iters), 0, float(sm_scale), int(num_splits), 1, _lib.ptr(ws.buffer), ws.nbytes,
+              int(iters), fitted_sink_tokens(), float(sm_scale), int(num_splits), 1,
+              _lib.ptr(ws.buffer), ws.nbytes,
               _lib.ptr(out), d, _lib.ptr(lse), _lib.ptr(csr_out), _lib.stream(dev))
     return PagedSparseAttentionResult(output=out, logsumexp=lse)

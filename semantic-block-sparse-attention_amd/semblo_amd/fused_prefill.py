@@ -14,6 +14,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+from .config import fitted_sink_tokens
 from .fused_select import theta_select_bitmask_flat
 from .kv_outer import dense_causal_attention, kv_outer_execute, kv_outer_plan
 
@@ -81,6 +82,22 @@ def chunk_window_start(chunk_start: int, target_tokens: int, dense_prefix_x: int
     return 0 if chunk_start <= cap else max(0, chunk_start - local)
 
 
+def hold_out_sink(sizes: torch.Tensor, target_tokens: int, sink: int) -> tuple[torch.Tensor, int]:
+    """The sizes the selection sees with the sink cluster 0 hidden (a copy: the attention
+    still reads cluster 0's rows), and the budget the other clusters share
+    (fused_prefill.py:202-209)."""
+    held = sizes.clone()
+    held[..., 0] = 0
+    return held, max(0, int(target_tokens) - int(sink))
+
+
+def force_sink_bit(*masks: torch.Tensor | None) -> None:
+    """Select cluster 0 in every row of every mask, in place (fused_prefill.py:212-216)."""
+    for m in masks:
+        if m is not None:
+            m[..., 0].bitwise_or_(1)
+
+
 def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, chunk_start: int,
                      chunk_end: int, *, temperature: float, beta: float, target_tokens: int,
                      queries_per_block: int = 32, iters: int = 16, local: int = 0,
@@ -103,10 +120,18 @@ def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, 
     bitmask = torch.zeros(nb, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
     qmask = torch.empty(q_count, hkv, c // 32, dtype=torch.int32, device=q_chunk.device)
     theta = torch.empty(q_count, hkv, dtype=torch.float32, device=q_chunk.device) if keep_theta else None
-    _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, causal_sizes[None],
+    # a sink (cluster 0, positions 0..S-1) is hidden from the search, which shares
+    # K - S among the other clusters, and then read by every query
+    # (fused_prefill.py:382-405)
+    sink = fitted_sink_tokens()
+    select_sizes, select_target = (hold_out_sink(causal_sizes, target_tokens, sink) if sink
+                                   else (causal_sizes, target_tokens))
+    _, tokens = theta_select_bitmask_flat(vectors, logmix, index.codebooks, select_sizes[None],
                                           bitmask, temperature=temperature, beta=beta,
-                                          target_tokens=target_tokens, g_union=g_union,
+                                          target_tokens=select_target, g_union=g_union,
                                           iters=iters, qmask=qmask, theta_out=theta)
+    if sink:
+        force_sink_bit(bitmask, qmask)
     kv = kv_outer_plan(qmask, causal_sizes, num_queries=q_count)
     return ChunkPlan(chunk_start, chunk_end, wstart, causal_sizes, tokens, kv, theta)
 

@@ -154,7 +154,7 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
               _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, _lib.ptr(queue), s)
     if timing is not None:
-        timing.begin(s)
+        timing.begin(s, "sparse")
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               _lib.ptr(packed_kv), packed_kv.shape[1], _lib.ptr(k_loc), _lib.ptr(v_loc),
               k_loc.stride(0), k_loc.stride(1), _lib.ptr(bucket_indptr), _lib.ptr(nvis), c,
@@ -201,7 +201,7 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(zero_counts),
               _lib.ptr(zero_counts), _lib.ptr(zero_counts), _lib.ptr(items), bound, _lib.ptr(queue), s)
     if timing is not None:
-        timing.begin(s)
+        timing.begin(s, "dense")
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
               None, 0, _lib.ptr(k), _lib.ptr(v), k.stride(0), k.stride(1), None, None, 32, None,
               None, _lib.ptr(items), _lib.ptr(queue), None, None,
@@ -222,15 +222,19 @@ class KernelTiming:
 
     def __init__(self, counts_flops: bool = True) -> None:
         self.events: list[tuple] = []
+        self.kinds: list = []
         self.flops: list = []
         self.counts_flops = counts_flops
 
-    def begin(self, stream_handle: int) -> None:
+    def begin(self, stream_handle: int, kind: str | None = None) -> None:
+        """``kind``: what the launch is (the attention's dense or sparse chunks), for a
+        split of the totals."""
         # the kernels launch on torch's current stream (the handle passed to libsbsa)
         assert stream_handle == torch.cuda.current_stream().cuda_stream
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         self.events.append([ev, None])
+        self.kinds.append(kind)
 
     def end(self, stream_handle: int) -> None:
         ev = torch.cuda.Event(enable_timing=True)
@@ -250,3 +254,14 @@ class KernelTiming:
 
     def total_flops(self) -> float:
         return float(sum(float(f) for f in self.flops))
+
+    def split(self, kind: str, steps: int = 1) -> tuple[float, int]:
+        """(ms per step, launches per step) of the launches of one kind."""
+        torch.cuda.synchronize()
+        sel = [i for i, k in enumerate(self.kinds) if k == kind]
+        ms = sum(self.events[i][0].elapsed_time(self.events[i][1]) for i in sel)
+        return ms / max(steps, 1), len(sel) // max(steps, 1)
+
+    def split_flops(self, kind: str) -> float:
+        """The FLOPs of the launches of one kind (one FLOP entry per launch)."""
+        return float(sum(float(f) for f, k in zip(self.flops, self.kinds) if k == kind))

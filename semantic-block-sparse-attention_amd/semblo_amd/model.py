@@ -97,6 +97,32 @@ class SembloAttention:
         self.arena = None
         return TokenOuterPrefillSession(self, tokens, chunk, **kw)
 
+    def begin_streamed_prefill(self, tokens: int):
+        """This layer's share of a layer-major streamed prefill of ``tokens`` positions:
+        ``keys`` for every slice, then ``ingest``, then ``queries`` for every slice
+        (the reference's layer.begin_streamed_prefill, model.py:1271-1279)."""
+        from .streamed_prefill import StreamedPrefillSession
+        return StreamedPrefillSession(self, tokens)
+
+    def prefill_streamed(self, q_post, q_pre, k_pre, k_post, v, output, slice_tokens: int,
+                         timing=None) -> torch.Tensor:
+        """The whole prompt through this layer in slices of ``slice_tokens``, keys pass then
+        queries pass (streamed_prefill.py:496-545, 710-736 for one layer)."""
+        length = q_post.shape[0]
+        hq, hkv, d = self.num_heads, self.num_kv_heads, self.head_dim
+        spans = [(s, min(length, s + slice_tokens)) for s in range(0, length, slice_tokens)]
+        session = self.begin_streamed_prefill(length)
+        for st, en in spans:
+            session.keys(k_pre.view(length, hkv, d)[st:en], k_post.view(length, hkv, d)[st:en],
+                         v.view(length, hkv, d)[st:en], st, en)
+        session.ingest()
+        out = output.view(length, hq, d)
+        for st, en in spans:
+            session.queries(q_post.view(length, hq, d)[st:en], q_pre.view(length, hq, d)[st:en], st,
+                            out=out[st:en], timing=timing)
+        session.finish()
+        return output
+
     def adopt_index(self, index: ProductPostingIndex) -> None:
         """Make a finished prompt index the layer's decode state."""
         cfg = self.runtime_config
@@ -129,6 +155,10 @@ class SembloAttention:
         if os.environ.get("SEMBLO_PREFILL_ORDER", "layer") == "token":
             chunk = int(os.environ.get("SEMBLO_PREFILL_CHUNK", "0") or 0) or cfg.query_chunk_size
             return self.prefill_token_order(q_post, q_pre, k_pre, k_post, v, output, chunk, timing=timing)
+        stream = int(os.environ.get("SEMBLO_PREFILL_CHUNK", "0") or 0)
+        if 0 < stream <= length:
+            # a long prefill streamed in slices, layer-major (PrefillStreamer.wants/run)
+            return self.prefill_streamed(q_post, q_pre, k_pre, k_post, v, output, stream, timing=timing)
         q = q_post.view(length, self.num_heads, self.head_dim)
         qp = q_pre.view(length, self.num_heads, self.head_dim)
         kp = k_pre.view(length, self.num_kv_heads, self.head_dim)
@@ -211,6 +241,13 @@ class SembloAttention:
         if self.arena is None:
             raise RuntimeError("decode before any prefill: the layer has no index")
         cfg = self.runtime_config
+        # The suffix store holds `reserve` generated positions (the reference sizes it to the
+        # model's room for generated tokens, arena.py:50-63); a step past it would neither
+        # store nor read its token, so it is refused here, counted on the host.
+        if self.arena.steps >= self.arena.reserve:
+            raise RuntimeError(f"the decode suffix holds {self.arena.reserve} generated positions "
+                               f"(suffix_reserve); raise it to the generation length")
+        self.arena.steps += 1
         fused_decode_step(self, self.arena, q_post=q_post, q_pre=q_pre, positions=positions,
                           k_post=k_post, v_states=v, output=output,
                           temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,

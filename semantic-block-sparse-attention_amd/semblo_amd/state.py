@@ -16,9 +16,17 @@ of empty clusters) come from a CPU ``torch.Generator`` seeded with
 keys' device; drawing on the CPU makes the partition independent of the
 device's RNG, and identical to the reference's own CPU build.  The
 reference reads the cluster counts every k-means iteration (its
-``empty.any()`` test); here the iterations run ahead and one read finds the
-first iteration that left a cluster empty, which is redone from there with
-the restart rows drawn, so the result is the same with fewer host reads.
+``empty.any()`` test).  Here the first RESTARTS_AHEAD restart draws of a head
+are made ahead and applied on the GPU at the first iterations that leave a
+cluster empty, the iterations run ahead, and one read of the counts tells
+how many draws were used: the generator's state is set back before the first
+unused one, and a later empty iteration is redone from there with its draw
+made then.  The draws and the result are the reference's, with one host read
+per head.
+
+With an attention sink (SEMBLO_SINK_TOKENS=S, state.py:757-782) positions
+0..S-1 form cluster 0, whose descriptor is zero, and the other positions are
+fitted into clusters 1..C-1 by the same k-means over C-1 centroids.
 """
 from __future__ import annotations
 
@@ -28,9 +36,11 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
-from .config import num_flat_clusters
+from .config import check_sink_partition, fitted_sink_tokens, num_flat_clusters
 
 PACK_ALIGN = 256
+# restart draws of the k-means fit made ahead per KV head (the GPU applies them)
+RESTARTS_AHEAD = 2
 
 
 class _DrawBuffers:
@@ -39,9 +49,13 @@ class _DrawBuffers:
     and the sample and initial rows go to the device from pinned memory."""
 
     def __init__(self, length: int, fit_n: int, c: int):
+        self.sub = torch.empty(fit_n, dtype=torch.int64)        # a host-side restart's draw
+        # a head's draws: sample permutation, init rows, restart rows drawn ahead
         self.perm = torch.empty(length, dtype=torch.int64)
-        self.sub = torch.empty(fit_n, dtype=torch.int64)
-        self.pinned = torch.empty(fit_n + c, dtype=torch.int32, pin_memory=True)
+        self.init = torch.empty(fit_n, dtype=torch.int64)
+        self.restarts = torch.empty(RESTARTS_AHEAD, fit_n, dtype=torch.int64)
+        self.pinned = torch.empty(fit_n + (1 + RESTARTS_AHEAD) * c, dtype=torch.int32,
+                                  pin_memory=True)
         self.uploaded = None            # event after the last upload from `pinned`
         self.counts = None              # pinned [iterations, C] cluster counts
 
@@ -108,7 +122,7 @@ class ProductPostingIndex:
               descriptor_weight=None, descriptor_bias=None, descriptor_activation: str = "softplus",
               layer_idx: int | None = None, router_pass: bool = False,
               fit_iters: int | None = None, num_clusters: int | None = None,
-              fit_trace: list | None = None) -> "ProductPostingIndex":
+              fit_trace: list | None = None, sink_tokens: int | None = None) -> "ProductPostingIndex":
         """Fit the flat codebook and the posting lists (state.py:477-542 contract).
 
         ``product_keys`` [L, Hkv, I] bf16 are the key router's output (or, with
@@ -122,7 +136,11 @@ class ProductPostingIndex:
         intermediate states (the key space, the sample rows, and per iteration
         the centroids it starts from, its assignment, sums and counts; then the
         final centroids and assignment of every key), for parity checks of each
-        k-means step.  The iterations then run one call at a time.
+        k-means step.  The iterations then run one call at a time.  With a sink the
+        fit covers positions S.. only, and so do the trace's rows, sample and final
+        assignment (cluster ids 0..C-2 of that fit).
+
+        ``sink_tokens``: S (None reads SEMBLO_SINK_TOKENS); 0 is the plain partition.
         """
         if product_keys.ndim != 3:
             raise ValueError("product_keys must have shape [L,Hkv,I]")
@@ -144,8 +162,15 @@ class ProductPostingIndex:
         iters = fit_iters if fit_iters is not None else int(os.environ.get("SEMBLO_FLAT_FIT_ITERS", "8"))
         per_c = int(os.environ.get("SEMBLO_FLAT_FIT_PER_C", "32"))
         align = int(os.environ.get("SEMBLO_FA3_ALIGN", page_align))
-        fit_n = min(length, max(int(kmeans_sample_size), per_c * c))
-        if fit_n < c:
+        sink = fitted_sink_tokens() if sink_tokens is None else int(sink_tokens)
+        if sink:
+            check_sink_partition(sink, length, length, c)
+        # the k-means runs over rows sink.. with cf centroids (ids 1.. of the partition
+        # when a sink holds cluster 0)
+        n_fit = length - sink
+        cf = c - 1 if sink else c
+        fit_n = min(n_fit, max(int(kmeans_sample_size), per_c * c))
+        if fit_n < cf:
             raise ValueError("sample must be at least as large as num_clusters")
         if c % 64 or c > 1024:
             raise ValueError(f"{c} clusters: the kernels take a multiple of 64 up to 1024")
@@ -159,12 +184,13 @@ class ProductPostingIndex:
 
         space_f32 = torch.empty(length, index_dim, dtype=torch.float32, device=dev)
         space_bf = torch.empty(length, index_dim, dtype=torch.bfloat16, device=dev)
-        cent_f32 = torch.empty(c, index_dim, dtype=torch.float32, device=dev)
-        cent_bf = torch.empty(c, index_dim, dtype=torch.bfloat16, device=dev)
+        cent_f32 = torch.empty(cf, index_dim, dtype=torch.float32, device=dev)
+        cent_bf = torch.empty(cf, index_dim, dtype=torch.bfloat16, device=dev)
         n_it = max(iters, 1)
-        sums_hist = torch.empty(n_it, c, index_dim, dtype=torch.float32, device=dev)
-        counts_hist = torch.empty(n_it, c, dtype=torch.int32, device=dev)
-        no_restart = torch.full((c,), -1, dtype=torch.int32, device=dev)
+        sums_hist = torch.empty(n_it, cf, index_dim, dtype=torch.float32, device=dev)
+        counts_hist = torch.empty(n_it, cf, dtype=torch.int32, device=dev)
+        no_restart = torch.full((cf,), -1, dtype=torch.int32, device=dev)
+        restart_flags = torch.zeros(n_it + 1, dtype=torch.int32, device=dev)   # [0] stays 0
         assign_s = torch.empty(fit_n, dtype=torch.int32, device=dev)
         assign_all = torch.empty(length, dtype=torch.int32, device=dev)
         cap = length + c * (max(align, 1) - 1)
@@ -174,99 +200,157 @@ class ProductPostingIndex:
         indptr = torch.empty(hkv, c + 1, dtype=torch.int32, device=dev)
         totals = torch.empty(hkv, dtype=torch.int32, device=dev)
         codebooks = torch.empty(hkv, 2, c, index_dim // 2, dtype=product_keys.dtype, device=dev)
+        desc_fit = torch.empty(2, cf, index_dim // 2, dtype=product_keys.dtype, device=dev) if sink else None
+        # the rows the k-means sees: positions sink..
+        fit_f32, fit_bf = space_f32[sink:], space_bf[sink:]
+        bits_bytes = _lib.query("sbsa_kmeans_member_bits_bytes", fit_n, cf)
+        member_bits = torch.empty(bits_bytes // 4, dtype=torch.int32, device=dev)
         ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
-        host = _draw_buffers(length, fit_n, c)
-        counts_host = host.counts_host(n_it, c)
+        host = _draw_buffers(n_fit, fit_n, cf)
+        counts_host = host.counts_host(n_it, cf)
 
-        def draw_sample_and_init():
-            # fit_flat_codebook's first two draws (flat_index.py:237-262)
-            torch.randperm(length, generator=gen, out=host.perm)
-            torch.randperm(fit_n, generator=gen, out=host.sub)
+        k_ahead = RESTARTS_AHEAD
+
+        def draw():
+            """fit_flat_codebook's first two draws (flat_index.py:237-262), then the
+            draws of the first k_ahead restarts (flat_index.py:277-283) made ahead: the
+            GPU applies the k-th at the k-th iteration that leaves a cluster empty.
+            Returns the generator's state before each restart draw, to take back the
+            draws no iteration needs, and uploads the draws from pinned memory."""
+            torch.randperm(n_fit, generator=gen, out=host.perm)
+            torch.randperm(fit_n, generator=gen, out=host.init)
+            before = []
+            for k in range(k_ahead):
+                before.append(gen.get_state())
+                torch.randperm(fit_n, generator=gen, out=host.restarts[k])
             if host.uploaded is not None:
                 host.uploaded.synchronize()     # the previous upload has left `pinned`
+            total = fit_n + (1 + k_ahead) * cf
             host.pinned[:fit_n].copy_(host.perm[:fit_n])
-            host.pinned[fit_n:].copy_(host.sub[:c])
-            both = torch.empty(fit_n + c, dtype=torch.int32, device=dev)
-            both.copy_(host.pinned, non_blocking=True)
+            host.pinned[fit_n:fit_n + cf].copy_(host.init[:cf])
+            host.pinned[fit_n + cf:total].view(k_ahead, cf).copy_(host.restarts[:, :cf])
+            both = torch.empty(total, dtype=torch.int32, device=dev)
+            both.copy_(host.pinned[:total], non_blocking=True)
             host.uploaded = torch.cuda.Event()
             host.uploaded.record()
-            return both[:fit_n], both[fit_n:]
+            return both[:fit_n], both[fit_n:fit_n + cf], both[fit_n + cf:], before
 
         steps: dict = {}
 
-        def iterate(start, sample_idx):
-            # k-means steps start.. with no restart rows, in one call; an iteration
-            # that left a cluster empty is found afterwards from counts_hist and redone
+        def iterate(start, sample_idx, restart_rows=None):
+            # k-means steps start.. in one call.  With restart_rows the first k_ahead
+            # iterations that leave clusters empty restart them on the GPU; an iteration
+            # that left a cluster empty without a restart is found afterwards from
+            # counts_hist and redone
+            def call(i0, i1):
+                _lib.call("sbsa_kmeans_iterate", _lib.ptr(fit_bf), _lib.ptr(fit_f32), index_dim,
+                          _lib.ptr(sample_idx), fit_n, cf, index_dim, _lib.ptr(assign_s),
+                          _lib.ptr(sums_hist), _lib.ptr(counts_hist), _lib.ptr(no_restart),
+                          _lib.ptr(restart_rows), k_ahead, _lib.ptr(restart_flags), _lib.ptr(cent_f32),
+                          _lib.ptr(cent_bf), _lib.ptr(member_bits), bits_bytes, i0, i1, s)
             if fit_trace is not None:
                 for i in range(start, iters):
                     entry = cent_bf.clone()
-                    _lib.call("sbsa_kmeans_iterate", _lib.ptr(space_bf), _lib.ptr(space_f32),
-                              index_dim, _lib.ptr(sample_idx), fit_n, c, index_dim,
-                              _lib.ptr(assign_s), _lib.ptr(sums_hist), _lib.ptr(counts_hist),
-                              _lib.ptr(no_restart), _lib.ptr(cent_f32), _lib.ptr(cent_bf), i,
-                              i + 1, s)
+                    call(i, i + 1)
                     steps[i] = (entry, assign_s.clone())
                 return
             if start < iters:
-                _lib.call("sbsa_kmeans_iterate", _lib.ptr(space_bf), _lib.ptr(space_f32), index_dim,
-                          _lib.ptr(sample_idx), fit_n, c, index_dim, _lib.ptr(assign_s),
-                          _lib.ptr(sums_hist), _lib.ptr(counts_hist), _lib.ptr(no_restart),
-                          _lib.ptr(cent_f32), _lib.ptr(cent_bf), start, iters, s)
+                call(start, iters)
 
-        def first_empty(it0):
-            """The first iteration >= it0 that left a cluster empty, or -1 (one host read)."""
-            counts_host[it0:iters].copy_(counts_hist[it0:iters])
-            torch.cuda.current_stream(dev).synchronize()
+        def read_counts(it0):
+            """Copy the counts of iterations it0.. to the host; the event marks their arrival."""
+            counts_host[it0:iters].copy_(counts_hist[it0:iters], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            return ev
+
+        def empty_iterations(it0):
+            """The iterations >= it0 that left a cluster empty (the counts are on the host)."""
             hit = torch.nonzero((counts_host[it0:iters] == 0).any(dim=1)).flatten()
-            return it0 + int(hit[0]) if hit.numel() else -1
+            return [it0 + int(i) for i in hit]
 
-        draws = draw_sample_and_init()
+        def finalize(h):
+            """Assign every key, lay the runs out, write the descriptor."""
+            _lib.call("sbsa_kmeans_assign", _lib.ptr(fit_bf), index_dim, None, n_fit,
+                      _lib.ptr(cent_bf), cf, index_dim, _lib.ptr(assign_all[sink:]), s)
+            fit_assign = None
+            if sink:
+                fit_assign = assign_all[sink:].clone() if fit_trace is not None else None
+                assign_all[sink:] += 1          # clusters 1..C-1
+                assign_all[:sink] = 0           # the sink
+            _lib.call("sbsa_bucket_layout", _lib.ptr(assign_all), length, c, max(align, 1),
+                      _lib.ptr(sizes[h]), _lib.ptr(indptr[h]), _lib.ptr(posting_full[h]), cap,
+                      _lib.ptr(inverse[h]), _lib.ptr(totals[h:h + 1]), _lib.ptr(ws), ws_bytes, s)
+            if sink:
+                # cluster 0's descriptor is zero: no score lands there, no key joins it later
+                _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
+                          cf, index_dim, None, _lib.ptr(desc_fit), s)
+                codebooks[h, :, 1:].copy_(desc_fit)
+                codebooks[h, :, 0].zero_()
+            else:
+                _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
+                          c, index_dim, None, _lib.ptr(codebooks[h]), s)
+            return fit_assign
+
+        sample_idx, init, restart_rows, before_restart = draw()
         for h in range(hkv):
             kh = pk[:, h]
             _lib.call("sbsa_key_space", _lib.ptr(kh), length, kh.stride(0), index_dim,
                       int(bool(router_pass)), _lib.ptr(space_f32), _lib.ptr(space_bf), s)
-            sample_idx, init = draws
-            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(space_f32),
-                      index_dim, _lib.ptr(sample_idx), c, index_dim, _lib.ptr(cent_f32),
+            _lib.call("sbsa_kmeans_centroids", 0, None, None, _lib.ptr(init), _lib.ptr(fit_f32),
+                      index_dim, _lib.ptr(sample_idx), cf, index_dim, _lib.ptr(cent_f32),
                       _lib.ptr(cent_bf), s)
-            iterate(0, sample_idx)
-            it = first_empty(0) if iters > 0 else -1
+            iterate(0, sample_idx, restart_rows)
+            counted = read_counts(0) if iters > 0 else None
+            # the final steps are enqueued now, and again if an empty iteration past
+            # those restarted on the GPU is redone below
+            fit_assign = finalize(h)
+            # The next head's draws wait for this head's counts: they follow the restart
+            # draws this head takes, and drawing ahead for a guessed outcome costs host
+            # time the GPU then waits for
+            if counted is not None:
+                counted.synchronize()
+            empties = empty_iterations(0) if iters > 0 else []
+            if len(empties) < k_ahead:
+                gen.set_state(before_restart[len(empties)])   # take back the unused draws
+            # the GPU restarted the first k_ahead empty iterations; the next is restarted here
+            it = empties[k_ahead] if len(empties) > k_ahead else -1
             while it >= 0:
                 # the reference's restart of the empty clusters at iteration it
                 # (flat_index.py:277-283), then the later iterations again
                 empty = counts_host[it] == 0
-                src = torch.full((c,), -1, dtype=torch.int32)
+                src = torch.full((cf,), -1, dtype=torch.int32)
                 torch.randperm(fit_n, generator=gen, out=host.sub)
                 src[empty] = host.sub[:int(empty.sum())].to(torch.int32)
                 src_d = src.to(dev)
                 _lib.call("sbsa_kmeans_centroids", 1, _lib.ptr(sums_hist[it]), _lib.ptr(counts_hist[it]),
-                          _lib.ptr(src_d), _lib.ptr(space_f32), index_dim, _lib.ptr(sample_idx),
-                          c, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
+                          _lib.ptr(src_d), _lib.ptr(fit_f32), index_dim, _lib.ptr(sample_idx),
+                          cf, index_dim, _lib.ptr(cent_f32), _lib.ptr(cent_bf), s)
                 iterate(it + 1, sample_idx)
-                it = first_empty(it + 1) if it + 1 < iters else -1
-            # assign every key, lay the runs out, descriptor
-            _lib.call("sbsa_kmeans_assign", _lib.ptr(space_bf), index_dim, None, length,
-                      _lib.ptr(cent_bf), c, index_dim, _lib.ptr(assign_all), s)
-            _lib.call("sbsa_bucket_layout", _lib.ptr(assign_all), length, c, max(align, 1),
-                      _lib.ptr(sizes[h]), _lib.ptr(indptr[h]), _lib.ptr(posting_full[h]), cap,
-                      _lib.ptr(inverse[h]), _lib.ptr(totals[h:h + 1]), _lib.ptr(ws), ws_bytes, s)
-            _lib.call("sbsa_kmeans_centroids", 2, _lib.ptr(cent_f32), None, None, None, 0, None,
-                      c, index_dim, None, _lib.ptr(codebooks[h]), s)
+                if it + 1 < iters:
+                    read_counts(it + 1).synchronize()
+                    later = empty_iterations(it + 1)
+                    it = later[0] if later else -1
+                else:
+                    it = -1
+                if it < 0:
+                    fit_assign = finalize(h)
             if fit_trace is not None:
+                # copies (a tensor already on the host would otherwise be the reused buffer)
                 fit_trace.append(dict(
-                    space_f32=space_f32.cpu(), space_bf16=space_bf.cpu(),
-                    sample=sample_idx.cpu().long(),
-                    entry_centroids=[steps[i][0].cpu() for i in range(iters)],
-                    assign=[steps[i][1].cpu().long() for i in range(iters)],
-                    sums=sums_hist[:iters].cpu(), counts=counts_hist[:iters].cpu(),
-                    final_centroids_f32=cent_f32.cpu(), final_centroids=cent_bf.cpu(),
-                    final_assign=assign_all.cpu().long()))
+                    space_f32=fit_f32.to('cpu', copy=True), space_bf16=fit_bf.to('cpu', copy=True), sink=sink,
+                    sample=sample_idx.to('cpu', copy=True).long(),
+                    entry_centroids=[steps[i][0].to('cpu', copy=True) for i in range(iters)],
+                    assign=[steps[i][1].to('cpu', copy=True).long() for i in range(iters)],
+                    sums=sums_hist[:iters].to('cpu', copy=True), counts=counts_hist[:iters].to('cpu', copy=True),
+                    final_centroids_f32=cent_f32.to('cpu', copy=True), final_centroids=cent_bf.to('cpu', copy=True),
+                    final_assign=(fit_assign if sink else assign_all).to('cpu', copy=True).long(),
+                    partition=assign_all.to('cpu', copy=True).long()))
                 steps.clear()
             if h + 1 < hkv:
-                # the next head's draws, on the host while the GPU lays this head out
-                draws = draw_sample_and_init()
+                sample_idx, init, restart_rows, before_restart = draw()
         width = int(totals.max().item())
         posting = posting_full[:, :width].contiguous()
         return cls(codebooks=codebooks, posting_positions=posting, bucket_indptr=indptr,

@@ -204,6 +204,7 @@ def gpu_tests(*node_ids: str) -> None:
     run unchanged, every kernel under the address sanitizer."""
     import importlib
     import pytest
+    sys.path.insert(0, str(TESTS / "golden"))      # as tests/conftest.py does
     for node in node_ids:
         mod = importlib.import_module(Path(node.split("::")[0]).stem)
         mod.DEV = "cpu"

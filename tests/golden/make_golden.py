@@ -11,7 +11,8 @@ the vectors are kept.
 
   kmeans_*.pt   ProductPostingIndex.build (state.py:477-948) on CPU, paper
                 settings (flat unit 2048, whole routing, 8 fit iterations,
-                page alignment 16).  The keys are regenerated from the seed by
+                page alignment 16); kmeans_sink* with SEMBLO_SINK_TOKENS set
+                (cluster 0 reserved for the first positions).  The keys are regenerated from the seed by
                 tests/golden/synth.py; a checksum of them is stored.
   router_*.pt   trivial_router_vectors (trivial_router.py:48-75) through its
                 torch path off the GPU (:55-61), on seeded bf16 queries with
@@ -76,6 +77,51 @@ def make_kmeans(ref_root: str) -> None:
         torch.save(out, HERE / f"{name}.pt")
         print(name, "C =", int(index.bucket_sizes.shape[1]), "width =",
               int(index.posting_positions.shape[1]))
+
+
+KMEANS_SINK_CASES = [
+    # name, L, Hkv, D, seed, codebook_seed, min_log2, sink (SEMBLO_SINK_TOKENS)
+    ("kmeans_sink32_l2048_d128", 2048, 2, 128, 14, 5, 5, 32),
+    ("kmeans_sink64_l4096_d128", 4096, 1, 128, 15, 1, 7, 64),
+]
+
+
+def make_kmeans_sink(ref_root: str) -> None:
+    """The fitted partition with an attention sink (state.py:757-782): positions
+    0..S-1 are cluster 0, the others fitted into C-1 clusters."""
+    os.environ.update({
+        "SEMBLO_FLAT_UNIT_TOKENS": "2048",
+        "SEMBLO_FA3_ALIGN": "16",
+        "SEMBLO_ROUTING_NORMALIZE": "whole",
+    })
+    from semblo.vllm_plugin.routing_map import routing_normalize
+    from semblo.vllm_plugin.state import ProductPostingIndex
+    for name, length, hkv, d, seed, cseed, min_log2, sink in KMEANS_SINK_CASES:
+        os.environ["SEMBLO_FLAT_MIN_CLUSTERS_LOG2"] = str(min_log2)
+        os.environ["SEMBLO_SINK_TOKENS"] = str(sink)
+        try:
+            k_pre = golden_keys(length, hkv, d, seed, mixture=name.endswith("_mix"))
+            product = routing_normalize(k_pre, 2)
+            index = ProductPostingIndex.build(
+                product, torch.arange(length), num_centroids=128, kmeans_iters=4,
+                kmeans_sample_size=8192, codebook_seed=cseed, flat_unit_tokens=2048,
+                flat_min_clusters_log2=min_log2, page_align=16)
+        finally:
+            os.environ.pop("SEMBLO_SINK_TOKENS", None)
+        out = dict(
+            length=torch.tensor(length), hkv=torch.tensor(hkv), d=torch.tensor(d),
+            seed=torch.tensor(seed), codebook_seed=torch.tensor(cseed),
+            min_log2=torch.tensor(min_log2), sink=torch.tensor(sink),
+            keys_checksum=keys_checksum(k_pre),
+            codebooks=index.codebooks.contiguous(),
+            posting=index.posting_positions.contiguous(),
+            indptr=index.bucket_indptr.contiguous(),
+            sizes=index.bucket_sizes.contiguous(),
+            inverse=index.inverse_positions().contiguous(),
+        )
+        torch.save(out, HERE / f"{name}.pt")
+        print(name, "C =", int(index.bucket_sizes.shape[1]), "sink size",
+              index.bucket_sizes[:, 0].tolist())
 
 
 SELECT_CASES = [
@@ -167,6 +213,8 @@ if __name__ == "__main__":
     which = sys.argv[2] if len(sys.argv) > 2 else "all"
     if which in ("all", "kmeans"):
         make_kmeans(ref)
+    if which in ("all", "kmeans_sink"):
+        make_kmeans_sink(ref)
     if which in ("all", "select"):
         make_select(ref)
     if which in ("all", "router"):

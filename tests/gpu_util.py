@@ -132,12 +132,21 @@ def cluster_position_mask(posting: torch.Tensor, indptr: torch.Tensor, counts: t
     return m
 
 
-def oracle_select(vectors, codebooks, sizes, *, temperature, beta, target, g_union=None):
-    """The oracle's scores and bisection; one size snapshot ([1, Hkv, C]) serves every query."""
+def oracle_select(vectors, codebooks, sizes, *, temperature, beta, target, g_union=None, sink=0):
+    """The oracle's scores and bisection; one size snapshot ([1, Hkv, C]) serves every query.
+    ``sink`` > 0: cluster 0 hidden from the search, the budget less the sink, then cluster
+    0 selected for every query (fused_prefill.py:382-405)."""
     prob = ref.mixture_probs(vectors.cpu(), None, codebooks.cpu(), temperature)
     if g_union is None:
         g_union = prob.shape[0] if sizes.shape[0] == 1 else 1
-    return ref.theta_select(prob, sizes.cpu(), beta=beta, target_tokens=target, g_union=max(g_union, 1))
+    sizes = sizes.cpu()
+    if sink:
+        sizes, target = ref.hold_out_sink(sizes, target, sink)
+    out = ref.theta_select(prob, sizes, beta=beta, target_tokens=target, g_union=max(g_union, 1))
+    if sink:
+        out["sel"][..., 0] = True
+        ref.force_sink_bit(out["qmask"], out["bitmask"])
+    return out
 
 
 # ---------------------------------------------------------------- k-means trace ----------
@@ -353,7 +362,7 @@ def decode_rows_reference(q: torch.Tensor, packed: torch.Tensor, indptr: torch.T
 def check_recorded_chunk(rec: dict, q: torch.Tensor, q_pre: torch.Tensor, k: torch.Tensor,
                          v: torch.Tensor, index, out: torch.Tensor, *, target: int,
                          rows: torch.Tensor | None = None, tau: float = 0.1, beta: float = 0.25,
-                         tag: str = "") -> dict:
+                         tag: str = "", sink: int = 0) -> dict:
     """One sparse chunk of a prefill, from its recorded plan (ChunkPlan.record): the
     attention of the sampled rows against fp64 over the GPU's own key sets, with no
     query off tolerance, and the GPU's selection against the oracle's (differences only
@@ -372,7 +381,7 @@ def check_recorded_chunk(rec: dict, q: torch.Tensor, q_pre: torch.Tensor, k: tor
     err = assert_close_bf16(out[cs + rows], want, f"{tag} chunk {cs}")
     vec = ref.trivial_router_vectors(q_pre[cs + rows], 1)
     exp = oracle_select(vec, index.codebooks.cpu(), sizes[None], temperature=tau, beta=beta,
-                        target=target)
+                        target=target, sink=sink)
     theta = rec["theta"].cpu()[rows] if rec.get("theta") is not None else None
     rep = compare_selection(sel, exp["sel"], exp["score"], exp["theta"], theta)
     rep["max_err"] = err

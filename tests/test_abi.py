@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
     for name, n in decls.items():
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
         assert len(_lib.SIGNATURES[name][1]) == n, f"{name}: header {n} args, binding {len(_lib.SIGNATURES[name][1])}"
-    assert lib.sbsa_abi_version() == 3
+    assert lib.sbsa_abi_version() == 4
 
 
 def test_size_queries_run_without_a_gpu():
@@ -71,7 +71,17 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     lib = _lib.load()
     p = 256                                   # stand-in for a device pointer
     # k-means iterations it0..it1 with it1 < it0
-    assert lib.sbsa_kmeans_iterate(p, p, 256, p, 100, 64, 256, p, p, p, p, p, p, 3, 2, None) == 1
+    assert lib.sbsa_kmeans_iterate(p, p, 256, p, 100, 64, 256, p, p, p, p, None, 0, None, p, p, p,
+                                   1 << 20, 3, 2, None) == 1
+    # restart rows without their flags, and with no draws
+    assert lib.sbsa_kmeans_iterate(p, p, 256, p, 100, 64, 256, p, p, p, None, p, 2, None, p, p, p,
+                                   1 << 20, 0, 2, None) == 1
+    assert lib.sbsa_kmeans_iterate(p, p, 256, p, 100, 64, 256, p, p, p, None, p, 0, p, p, p, p,
+                                   1 << 20, 0, 2, None) == 1
+    # the update's member bitmaps smaller than the bound
+    need = lib.sbsa_kmeans_member_bits_bytes(1000, 64)
+    assert need == 64 * 32 * 4
+    assert lib.sbsa_kmeans_update(p, 256, p, 1000, p, 64, 256, p, p, p, need - 1, None) == 4
     # the work list without the reverse index's arrays
     assert lib.sbsa_prefill_items(p, 4, 64, 128, 32, 1, None, p, p, p, 100, p, None) == 1
     # a window that starts after the chunk

@@ -145,3 +145,29 @@ def test_decode_step_replays_in_a_hip_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(s_out, eager[t]), f"replay {t} differs from the eager step"
+
+
+def test_layer_decode_refuses_a_step_past_the_suffix_reserve():
+    """The suffix store holds suffix_reserve generated positions; the layer's decode
+    refuses the step after them instead of dropping its token (counted on the host)."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.model import SembloAttention
+    from semblo_amd.synthetic import decode_queries, mixture_layer
+    length, hq, hkv, d, reserve = 1024, 8, 2, 128, 32
+    cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=512,
+                              suffix_reserve=reserve)
+    layer = SembloAttention(cfg, layer_name="test.decode.reserve")
+    inp = mixture_layer(length, hq, hkv, d, mixtures=16, seed=8)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    out = torch.empty(length, hq * d, dtype=torch.bfloat16, device=DEV)
+    layer.prefill(q, q, k, k, v, out)
+    qs, kn, vn = decode_queries(inp, reserve + 1, hq, seed=8)
+    dec = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
+    for t in range(reserve):
+        pos = torch.tensor([length + t], dtype=torch.int32, device=DEV)
+        layer.decode(pos, qs[t:t + 1].to(DEV), qs[t:t + 1].to(DEV), kn[t:t + 1].to(DEV),
+                     vn[t:t + 1].to(DEV), dec)
+    torch.cuda.synchronize()
+    pos = torch.tensor([length + reserve], dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="suffix_reserve"):
+        layer.decode(pos, qs[-1:].to(DEV), qs[-1:].to(DEV), kn[-1:].to(DEV), vn[-1:].to(DEV), dec)

@@ -62,12 +62,13 @@ def _check_index_invariants(idx, length):
         assert (seen == 1).all(), "every position in exactly one cluster"
 
 
-def _traced_builds(product, codebook_seed, **kw):
+def _traced_builds(product, codebook_seed, sink=0, **kw):
     """The GPU build with its fit trace, and the oracle's build with its steps."""
     trace = []
-    idx = _build_gpu(product, codebook_seed=codebook_seed, fit_trace=trace, **kw)
+    idx = _build_gpu(product, codebook_seed=codebook_seed, fit_trace=trace, sink_tokens=sink, **kw)
     steps = []
     want = ref.build_flat_index(product, codebook_seed=codebook_seed, fit_steps=steps,
+                               sink_tokens=sink,
                                **({"min_clusters_log2": kw["flat_min_clusters_log2"]}
                                   if "flat_min_clusters_log2" in kw else {}))
     return idx, trace, want, steps
@@ -79,11 +80,16 @@ def _check_trace(product, idx, trace, want, steps, tag):
     reps = []
     posting_gpu = idx.posting_positions.cpu()
     for h, (tr, st) in enumerate(zip(trace, steps)):
-        rep = check_fit_trace(product[:, h], tr, st["steps"], st["final_assign"],
+        sink = int(tr.get("sink", 0))
+        # with a sink the fit (and its trace) covers positions sink.. only
+        rep = check_fit_trace(product[sink:, h], tr, st["steps"], st["final_assign"],
                               st["final_centroids"], tag=f"{tag} head {h}")
         reps.append(rep)
         # the bucket layout of the GPU's assignment is the oracle's layout of it, bit for bit
-        a = tr["final_assign"]
+        a = tr["partition"]
+        if sink:
+            assert torch.equal(a[:sink], torch.zeros(sink, dtype=a.dtype))
+            assert torch.equal(a[sink:], tr["final_assign"] + 1)
         order = torch.argsort(a, stable=True)
         counts = torch.bincount(a, minlength=idx.num_buckets).to(torch.int32)
         length = a.numel()
@@ -106,8 +112,13 @@ def test_build_matches_the_reference_golden(name):
     length, hkv, d = int(g["length"]), int(g["hkv"]), int(g["d"])
     k_pre = golden_keys(length, hkv, d, int(g["seed"]), mixture=name.endswith("_mix.pt"))
     product = ref.routing_normalize_keys(k_pre)
-    idx, trace, want, steps = _traced_builds(product, int(g["codebook_seed"]),
+    sink = int(g["sink"]) if "sink" in g else 0
+    idx, trace, want, steps = _traced_builds(product, int(g["codebook_seed"]), sink=sink,
                                              flat_min_clusters_log2=int(g["min_log2"]))
+    if sink:
+        # cluster 0 holds positions 0..S-1 and nothing else; its descriptor is zero
+        assert (idx.bucket_sizes[:, 0].cpu() == sink).all()
+        assert torch.count_nonzero(idx.codebooks[:, :, 0].cpu()) == 0
     _check_index_invariants(idx, length)
     assert torch.equal(want["posting"], g["posting"])       # the oracle is the reference here
     reps = _check_trace(product, idx, trace, want, steps, name)
@@ -203,3 +214,44 @@ def test_build_with_empty_clusters_matches_the_oracle():
     if all(r["origin_flips"] == 0 for r in reps):
         assert gpu_empties == empties
         assert torch.equal(idx.posting_positions.cpu(), want["posting"])
+
+
+@pytest.mark.parametrize("dim", [256, 320])
+def test_update_sums_and_counts_each_cluster(dim):
+    """The centroid sums through the C-ABI on a skewed assignment: cluster 0 holds
+    most rows (more than the kernel lists at once, so it is summed in windows),
+    cluster 5 none, the row count is ragged and the rows are read through a row map.
+    Counts exact; each sum within fp32 summation-order error of the fp64 sum of its
+    rows (the bound the fit's trace check uses); a second call on stale scratch gives
+    the same bits."""
+    from semblo_amd import _lib
+    gen = torch.Generator().manual_seed(11)
+    # ragged (not a multiple of 512 rows), two segments of 32768 rows, cluster 0 past the
+    # kernel's 8192-entry member list within one segment
+    rows, n, c = 48000, 40000 + 37, 64
+    x = torch.randn(rows, dim, generator=gen)
+    row_index = torch.randperm(rows, generator=gen)[:n].to(torch.int32)
+    assign = torch.randint(1, c, (n,), generator=gen, dtype=torch.int32)
+    assign[torch.rand(n, generator=gen) < 0.7] = 0
+    assign[assign == 5] = 6
+    xd, rd, ad = x.to(DEV), row_index.to(DEV), assign.to(DEV)
+    sums = torch.full((c, dim), float("nan"), device=DEV)
+    counts = torch.full((c,), -1, dtype=torch.int32, device=DEV)
+    nbytes = _lib.query("sbsa_kmeans_member_bits_bytes", n, c)
+    bits = torch.full((nbytes // 4,), -1, dtype=torch.int32, device=DEV)    # stale contents
+    _lib.call("sbsa_kmeans_update", _lib.ptr(xd), dim, _lib.ptr(rd), n, _lib.ptr(ad), c, dim,
+              _lib.ptr(sums), _lib.ptr(counts), _lib.ptr(bits), nbytes, _lib.stream(xd.device))
+    torch.cuda.synchronize()
+    first = sums.clone()
+    _lib.call("sbsa_kmeans_update", _lib.ptr(xd), dim, _lib.ptr(rd), n, _lib.ptr(ad), c, dim,
+              _lib.ptr(sums), _lib.ptr(counts), _lib.ptr(bits), nbytes, _lib.stream(xd.device))
+    torch.cuda.synchronize()
+    assert torch.equal(sums, first)
+    want = torch.zeros(c, dim, dtype=torch.float64).index_add_(0, assign.long(),
+                                                               x[row_index.long()].double())
+    cnt = torch.bincount(assign.long(), minlength=c)
+    assert int(cnt[:1]) > 2 * 8192 and int(cnt[5]) == 0
+    assert torch.equal(counts.cpu(), cnt.to(torch.int32))
+    scale = cnt.clamp_min(1).double()[:, None]
+    assert float(((sums.cpu().double() - want).abs() / scale).max()) <= 1e-5
+    assert torch.count_nonzero(sums[5]) == 0

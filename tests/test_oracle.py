@@ -33,7 +33,8 @@ def test_block_build_matches_the_reference_bit_for_bit(name):
     if "product" in g:
         assert torch.equal(product, g["product"])
     idx = ref.build_flat_index(product, codebook_seed=int(g["codebook_seed"]),
-                               min_clusters_log2=int(g["min_log2"]))
+                               min_clusters_log2=int(g["min_log2"]),
+                               sink_tokens=int(g["sink"]) if "sink" in g else 0)
     assert torch.equal(idx["sizes"], g["sizes"])
     assert torch.equal(idx["indptr"], g["indptr"])
     assert torch.equal(idx["posting"], g["posting"])
@@ -235,3 +236,51 @@ def test_relayout_keeps_each_key_at_its_offset_in_the_new_run():
     new = ref.relayout_rows(old_rows, old_ip, new_ip)
     assert new.tolist() == [[0, 64, 1, 65, 66, 2, 67, 68]]
     assert int(sizes.sum()) == new.shape[1]
+
+
+def test_sink_partition_properties():
+    """The reference's own sink tests (tests/test_fitted_sink.py:62-82) on the oracle:
+    positions < S are exactly cluster 0, in order, and nothing else is; cluster 0's
+    descriptor is zero and every used cluster's is not."""
+    sink = 32
+    k = torch.randn(512, 2, 16, generator=torch.Generator().manual_seed(0))
+    product = ref.routing_normalize_keys(k.to(torch.bfloat16))
+    idx = ref.build_flat_index(product, unit_tokens=16, min_clusters_log2=3, sample_size=256,
+                               fit_iters=2, sink_tokens=sink)
+    for h in range(2):
+        ip, sz, post = idx["indptr"][h], idx["sizes"][h], idx["posting"][h]
+        assert torch.equal(post[int(ip[0]):int(ip[0]) + int(sz[0])], torch.arange(sink, dtype=torch.int32))
+        for c in range(1, sz.numel()):
+            assert bool((post[int(ip[c]):int(ip[c]) + int(sz[c])] >= sink).all())
+        assert int(sz.sum()) == 512
+    cb = idx["codebooks"].float()
+    assert torch.count_nonzero(cb[:, :, 0]) == 0
+    used = idx["sizes"][:, 1:] > 0
+    assert bool((cb[:, :, 1:].norm(dim=-1).sum(1)[used] > 0).all())
+
+
+@pytest.mark.parametrize("sink, length, match", [(24, 512, "multiple of 16"), (512, 512, "too few keys"),
+                                                 (496, 512, "too few keys")])
+def test_sink_settings_that_do_not_compose_are_refused(sink, length, match):
+    """state.py:26-34 (the refusals of tests/test_fitted_sink.py:85-97 that apply here)."""
+    k = torch.randn(length, 1, 16, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match=match):
+        ref.build_flat_index(ref.routing_normalize_keys(k), unit_tokens=16, min_clusters_log2=3,
+                             sample_size=256, fit_iters=2, sink_tokens=sink)
+
+
+def test_sink_hold_out_and_forced_bit_known_answers():
+    """tests/test_fitted_sink.py:100-117 of the reference: the selector's view hides
+    cluster 0, the budget shrinks by S, the caller's sizes are untouched, and the forced
+    bit is bit 0 of word 0 (other bits untouched)."""
+    sizes = torch.tensor([[[32, 10, 0, 7]], [[32, 3, 5, 0]]], dtype=torch.int32)
+    held, target = ref.hold_out_sink(sizes, 100, 32)
+    assert target == 68
+    assert (held[..., 0] == 0).all() and torch.equal(held[..., 1:], sizes[..., 1:])
+    assert int(sizes[0, 0, 0]) == 32
+    qmask = torch.zeros(3, 2, 2, dtype=torch.int32)
+    qmask[1, 0, 1] = 5
+    ref.force_sink_bit(qmask, None)
+    got = ref.unpack_bits(qmask, 64)
+    assert got[..., 0].all()
+    assert int(got[..., 1:].sum()) == 2
