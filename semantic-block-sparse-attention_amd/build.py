@@ -27,15 +27,12 @@ FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # packed fp32 arithmetic is disabled for every HIP object
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs (gfx950 MFMAs read and write either file): no
+    # AGPR copies around the VALU work on the S tiles
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I", str(HERE.parent / "include"),
     "-Wno-unused-result",
 ]
-# MFMA results in VGPRs (gfx950 MFMAs read and write either file): no AGPR
-# copies around the VALU work on MFMA results.  Not for the prefill attention,
-# whose O accumulators fill the accumulation registers (its S^T MFMAs are
-# written out with vector-register results instead).
-VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-AGPR_SOURCES = {"attention"}
 
 
 def hipcc() -> str:
@@ -47,8 +44,7 @@ def hipcc() -> str:
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    extra = [] if src.stem in AGPR_SOURCES else VGPR_FORM
-    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

@@ -298,8 +298,9 @@ __global__ __launch_bounds__(1024) void rev_scan_kernel(const int32_t* __restric
 // Work list of the KV-outer body, one segment per XCD so that the items that
 // read the same K/V (the query tiles of one KV head's window, the query tiles
 // of one cluster) run on one XCD and share its L2.  Items within a segment:
-// local-window items first (longest first), then cluster items in (head,
-// cluster) order.  Item = {head, cluster or -1, first query slot, query
+// local-window items first (longest first), then cluster items, longest
+// cluster first (visible rows descending, ties in (head, cluster) order), so
+// that the items claimed last, when the queues run dry, are the shortest.  Item = {head, cluster or -1, first query slot, query
 // count}.  queue = {n[8], off[8], counter[8]}; the counters are zeroed here.
 // One block: per-XCD counts, each source's first item (one pass of eight
 // per-segment wave scans over each round of 1024 sources), then one thread
@@ -315,8 +316,10 @@ struct ItemSource {
   int x, n, h, c, qb, qn;
 };
 
-__device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, int s, int nloc, int hkv,
-                                                  int C, int Qc, int QT) {
+// order: cluster sources by enumeration position e' = 8 r + x, the source of
+// rank r in segment x (every segment's sources keep their segment)
+__device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, const int* order, int s,
+                                                  int nloc, int hkv, int C, int Qc, int QT) {
   ItemSource r;
   const int nl = nloc * hkv;
   if (s < nl) {
@@ -328,7 +331,7 @@ __device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, int
     r.n = 1;
     r.x = local_xcd(r.h, tile, hkv);
   } else {
-    const int e = s - nl;
+    const int e = order[s - nl];
     r.h = e / C;
     r.c = e % C;
     r.qb = 0;
@@ -347,17 +350,34 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
                                                            PrefillItem* __restrict__ items,
                                                            int32_t* __restrict__ queue,
                                                            int64_t cap) {
-  extern __shared__ int s_first[];     // [nsrc] first item of each source
+  extern __shared__ int s_first[];     // [nsrc] first item of each source, then
+                                       // [hkv C] sort keys and [hkv C] source order
   __shared__ int cnt[8];
   __shared__ int base[8];
   __shared__ int wsum[16][8];
   const int nloc = has_local ? (Qc + QT - 1) / QT : 0;
-  const int nsrc = nloc * hkv + hkv * C;
+  const int ncl = hkv * C;
+  const int nsrc = nloc * hkv + ncl;
+  int* s_key = s_first + nsrc;
+  int* s_order = s_key + ncl;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (threadIdx.x < 8) cnt[threadIdx.x] = 0;
+  // cluster sources ranked within their segment (e & 7) by visible rows,
+  // descending; sources without queries last
+  for (int e = threadIdx.x; e < ncl; e += 1024) s_key[e] = rev_counts[e] > 0 ? nvis[e] : -1;
+  __syncthreads();
+  for (int e = threadIdx.x; e < ncl; e += 1024) {
+    const int k = s_key[e];
+    int rank = 0;
+    for (int e2 = e & 7; e2 < ncl; e2 += 8) {
+      const int k2 = s_key[e2];
+      rank += (k2 > k || (k2 == k && e2 < e)) ? 1 : 0;
+    }
+    s_order[8 * rank + (e & 7)] = e;
+  }
   __syncthreads();
   for (int s = threadIdx.x; s < nsrc; s += 1024) {
-    const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+    const ItemSource si = item_source(rev_counts, s_order, s, nloc, hkv, C, Qc, QT);
     if (si.n) atomicAdd(&cnt[si.x], si.n);
   }
   __syncthreads();
@@ -387,7 +407,7 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
     const int s = r0 + threadIdx.x;
     int n = 0, x = 0;
     if (s < nsrc) {
-      const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+      const ItemSource si = item_source(rev_counts, s_order, s, nloc, hkv, C, Qc, QT);
       n = si.n;
       x = si.x;
     }
@@ -414,7 +434,7 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
   }
   // expansion: one thread per source writes its items
   for (int s = threadIdx.x; s < nsrc; s += 1024) {
-    const ItemSource si = item_source(rev_counts, s, nloc, hkv, C, Qc, QT);
+    const ItemSource si = item_source(rev_counts, s_order, s, nloc, hkv, C, Qc, QT);
     if (!si.n) continue;
     int64_t f0 = s_first[s];
     int64_t rel = 0;
@@ -563,8 +583,8 @@ int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clus
   if (!rev_counts || !items || !queue || queries_per_item < 1) return SBSA_ERR_ARG;
   if (!indptr || !nvis || !rev_indptr) return SBSA_ERR_ARG;
   const int nloc = has_local ? (num_queries + queries_per_item - 1) / queries_per_item : 0;
-  const size_t lds = (size_t)(nloc * num_kv_heads + num_kv_heads * num_clusters) * 4;
-  if (lds > 96 * 1024) return SBSA_ERR_UNSUPPORTED;
+  const size_t lds = (size_t)(nloc * num_kv_heads + 3 * num_kv_heads * num_clusters) * 4;
+  if (lds > 150 * 1024) return SBSA_ERR_UNSUPPORTED;
   static size_t configured = 0;
   if (lds > configured) {
     if (hipFuncSetAttribute((const void*)build_items_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
