@@ -178,11 +178,9 @@ int sbsa_prefill_item_rows(void);
  * rev_indptr [Hkv*C + 1] are those later passed to sbsa_prefill_attend (any
  * valid arrays when no cluster has queries).  Items are grouped in one segment
  * per XCD (the query tiles of a KV head's window, and those of one cluster,
- * share an XCD and its L2); queue (int32[32 + items_cap]) receives the
- * segments' sizes and offsets and zeroed counters in its first 32 ints, and
- * holds from int 32 the list of items sbsa_prefill_attend recomputes (rows
- * whose probabilities passed the bound of their first tile's maximum).
- * queries_per_item = sbsa_prefill_item_rows() / (Hq/Hkv). */
+ * share an XCD and its L2), window items first (longest first), then cluster
+ * items, longest cluster first; queue (int32[24]) receives the segments' sizes
+ * and offsets and zeroed counters.  queries_per_item = 128 / (Hq/Hkv). */
 int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
                                  int num_clusters, int queries_per_item);
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,

@@ -395,10 +395,6 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
     queue[x] = (int32_t)max((int64_t)0, end - base[x]);   // n
     queue[8 + x] = base[x];                              // offset
     queue[16 + x] = 0;                                   // counter
-    if (x == 0) {
-      queue[24] = 0;                                     // overflow list: count
-      queue[25] = 0;                                     // and claim counter
-    }
   }
   // each source's first item: the segment's fill plus the items of the
   // segment's earlier sources, by one scan per segment over each round of

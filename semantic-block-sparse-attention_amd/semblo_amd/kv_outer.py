@@ -25,9 +25,6 @@ from . import _lib
 # int32 fields of one work item {head, cluster, first query slot, count,
 # visible rows, first partial slot, first packed row, 0}
 ITEM_INTS = 8
-# the work queue: 32 ints of counters, then room for an overflow list of up to
-# one entry per item (items the attention recomputes with their true row maxima)
-QUEUE_HEAD = 32
 
 
 def queries_per_item(q_per_kv: int) -> int:
@@ -149,7 +146,7 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     qt = queries_per_item(g)
     bound = _lib.query("sbsa_prefill_items_bound", cap, qn, hkv, c, qt)
     items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
-    queue = torch.empty(QUEUE_HEAD + max(bound, 1), dtype=torch.int32, device=dev)
+    queue = torch.empty(24, dtype=torch.int32, device=dev)
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
               _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, _lib.ptr(queue), s)
@@ -193,7 +190,7 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
     bound = hkv * ((qn + qt - 1) // qt) + 1
     items = torch.empty(bound, ITEM_INTS, dtype=torch.int32, device=dev)
-    queue = torch.empty(QUEUE_HEAD + bound, dtype=torch.int32, device=dev)
+    queue = torch.empty(24, dtype=torch.int32, device=dev)
     if out is None:
         out = torch.empty_like(q)
     s = _lib.stream(dev)
