@@ -454,6 +454,10 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
              f"{flops / 1e12:.2f} TFLOP -> {achieved:.1f} TFLOP/s ("
              + ", ".join(f"{k} chunks {v['ms']:.2f} ms, {v['achieved']:.0f} TFLOP/s" for k, v in by_form.items())
              + ")")
+        sess = getattr(layer, "last_session", None) if conf.get("order") == "token" else None
+        reruns = sess.guard.reruns if sess is not None else getattr(layer, "partials_reruns", 0)
+        result.update(partials_reruns=reruns)
+        _log(f"sparse chunks run again after passing the partial-buffer cap: {reruns} per layer")
         if store is not None:
             st_ms = store.total_ms()
             st_bytes = store.total_flops()           # the store timing collects bytes
@@ -514,6 +518,7 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
             "kernel": "attn_items_kernel<256,4,*> (dense chunks: compact form, sparse chunks: pipelined form)",
             "flops_per_layer": result["flops"], "kernel_ms_per_layer": round(result["attn_ms"], 3),
             "launches_per_layer": result["launches"],
+            "partials_reruns": result.get("partials_reruns", 0),
             "by_form": result.get("by_form")},
         "decode_roofline": None if "decode_us" not in result else {
             "bound": "hbm", "achieved": round(result["decode_gbs"], 1), "peak": PEAK_HBM_GBS,

@@ -179,14 +179,21 @@ int sbsa_prefill_item_rows(void);
  * valid arrays when no cluster has queries).  Items are grouped in one segment
  * per XCD (the query tiles of a KV head's window, and those of one cluster,
  * share an XCD and its L2), window items first (longest first), then cluster
- * items, longest cluster first; queue (int32[24]) receives the segments' sizes
- * and offsets and zeroed counters.  queries_per_item = 128 / (Hq/Hkv). */
+ * items, longest cluster first; queue (int32[32]) receives the segments' sizes
+ * and offsets and zeroed counters in ints 0-23, and in int 24 an overflow
+ * flag: with partials_cap > 0 and more partial entries than that
+ * (rev_indptr[Hkv*C] > partials_cap) the list is empty and the flag 1, so the
+ * attention writes nothing and sbsa_prefill_combine (given the flag) skips the
+ * chunk, which the caller runs again with a partial buffer of its exact size
+ * (the reference reads the count instead, kv_outer.py:592-613).
+ * queries_per_item = 128 / (Hq/Hkv). */
 int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
                                  int num_clusters, int queries_per_item);
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
                        int num_queries, int queries_per_item, int has_local,
                        const int32_t* indptr, const int32_t* nvis, const int32_t* rev_indptr,
-                       void* items, int64_t items_cap, int32_t* queue, hipStream_t stream);
+                       void* items, int64_t items_cap, int64_t partials_cap, int32_t* queue,
+                       hipStream_t stream);
 
 /* Attention over the work list (kv_outer.py:482-816; dense chunks:
  * fused_prefill.py:155-189).  q [Qc, Hq, dim] (strides q_sq, q_sh); packed
@@ -213,13 +220,15 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
  * Replaces combine_partials / _combine_grouped_kernel
  * (semblo/vllm_plugin/kv_outer.py:370-479): per (query, KV head), seeds with
  * the local window and folds the partials of the query's clusters in cluster
- * order by online log-sum-exp; out [Qc, Hq, dim] bf16, out_lse [Qc, Hq] or null. */
+ * order by online log-sum-exp; out [Qc, Hq, dim] bf16, out_lse [Qc, Hq] or null.
+ * skip (null, or the work list's overflow flag, queue + 24): a nonzero flag
+ * leaves out untouched. */
 int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_t* rev_indptr,
                          const int32_t* qrank, const void* part_o, const float* part_lse,
                          const void* local_o, int64_t lo_sq, int64_t lo_sh, const float* local_lse,
                          void* out, int64_t out_sq, int64_t out_sh, float* out_lse,
                          int num_queries, int num_q_heads, int num_kv_heads, int dim,
-                         int num_clusters, hipStream_t stream);
+                         int num_clusters, const int32_t* skip, hipStream_t stream);
 
 /* ---- S7-S9: decode step ------------------------------------------------------------
  * Replaces fused_decode_step (semblo/vllm_plugin/fused_decode.py:393-521): the

@@ -776,8 +776,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
     const bf16_t* __restrict__ part_o, const float* __restrict__ part_lse,
     const bf16_t* __restrict__ local_o, int64_t lo_sq, int64_t lo_sh,
     const float* __restrict__ local_lse, bf16_t* __restrict__ out, int64_t out_sq, int64_t out_sh,
-    float* __restrict__ out_lse, int Qc, int Hkv, int C) {
+    float* __restrict__ out_lse, int Qc, int Hkv, int C, const int32_t* __restrict__ skip) {
   constexpr int E = G * D / 64;
+  if (skip && *skip) return;   // the chunk's partials passed their buffer: it runs again
   static_assert(E >= 1 && D % E == 0, "lane share");
   __shared__ int s_list[4][COMBINE_MAX_LIST];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -907,11 +908,11 @@ int launch_combine(const int32_t* qmask, const int32_t* nvis, const int32_t* rev
                    const int32_t* qrank, const bf16_t* part_o, const float* part_lse,
                    const bf16_t* local_o, int64_t lo_sq, int64_t lo_sh, const float* local_lse,
                    bf16_t* out, int64_t out_sq, int64_t out_sh, float* out_lse, int Qc, int Hkv,
-                   int C, hipStream_t stream) {
+                   int C, const int32_t* skip, hipStream_t stream) {
   int64_t waves = (int64_t)Qc * Hkv;
   hipLaunchKernelGGL((combine_kernel<D, G>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
                      stream, qmask, nvis, rev_indptr, qrank, part_o, part_lse, local_o, lo_sq,
-                     lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C);
+                     lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C, skip);
   return SBSA_OK;
 }
 
@@ -936,9 +937,10 @@ int combine_dispatch(int D, int G, const int32_t* qmask, const int32_t* nvis,
                      const int32_t* rev_indptr, const int32_t* qrank, const bf16_t* part_o,
                      const float* part_lse, const bf16_t* local_o, int64_t lo_sq, int64_t lo_sh,
                      const float* local_lse, bf16_t* out, int64_t out_sq, int64_t out_sh,
-                     float* out_lse, int Qc, int Hkv, int C, hipStream_t stream) {
+                     float* out_lse, int Qc, int Hkv, int C, const int32_t* skip,
+                     hipStream_t stream) {
   SBSA_DISPATCH_DG(D, G, launch_combine, qmask, nvis, rev_indptr, qrank, part_o, part_lse, local_o,
-                   lo_sq, lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C, stream);
+                   lo_sq, lo_sh, local_lse, out, out_sq, out_sh, out_lse, Qc, Hkv, C, skip, stream);
 }
 
 }  // namespace
@@ -1008,7 +1010,7 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
                          const void* local_o, int64_t lo_sq, int64_t lo_sh, const float* local_lse,
                          void* out, int64_t out_sq, int64_t out_sh, float* out_lse,
                          int num_queries, int num_q_heads, int num_kv_heads, int dim,
-                         int num_clusters, hipStream_t stream) {
+                         int num_clusters, const int32_t* skip, hipStream_t stream) {
   if (!qmask || !nvis || !rev_indptr || !qrank || !local_o || !local_lse || !out) return SBSA_ERR_ARG;
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_clusters % 32) return SBSA_ERR_ARG;
   if (num_clusters > COMBINE_MAX_LIST) return SBSA_ERR_UNSUPPORTED;
@@ -1022,7 +1024,7 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
   int rc = combine_dispatch(dim, num_q_heads / num_kv_heads, qmask, nvis, rev_indptr, qrank,
                             (const bf16_t*)part_o, part_lse, (const bf16_t*)local_o, lo_sq, lo_sh,
                             local_lse, (bf16_t*)out, out_sq, out_sh, out_lse, num_queries,
-                            num_kv_heads, num_clusters, stream);
+                            num_kv_heads, num_clusters, skip, stream);
   if (rc) return rc;
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;

@@ -342,6 +342,10 @@ __device__ __forceinline__ ItemSource item_source(const int32_t* rev_counts, con
   return r;
 }
 
+// queue[QUEUE_OVERFLOW]: 1 when the chunk's partial entries pass the partial
+// buffer's capacity (the list is then empty)
+constexpr int QUEUE_OVERFLOW = 24;
+
 __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __restrict__ rev_counts,
                                                            int hkv, int C, int Qc, int QT,
                                                            int has_local, const int32_t* __restrict__ indptr,
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
                                                            const int32_t* __restrict__ rev_indptr,
                                                            PrefillItem* __restrict__ items,
                                                            int32_t* __restrict__ queue,
-                                                           int64_t cap) {
+                                                           int64_t cap, int64_t partials_cap) {
   extern __shared__ int s_first[];     // [nsrc] first item of each source, then
                                        // [hkv C] sort keys and [hkv C] source order
   __shared__ int cnt[8];
@@ -389,13 +393,19 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
     }
   }
   __syncthreads();
+  // a chunk whose partial entries (rev_indptr[hkv C]) pass the partial
+  // buffer's capacity gets an empty list and the overflow flag: nothing of it
+  // is written, and the caller runs it again with a buffer of its exact size
+  const bool overflow = partials_cap > 0 && (int64_t)rev_indptr[ncl] > partials_cap;
   if (threadIdx.x < 8) {
     const int x = threadIdx.x;
     const int64_t end = min((int64_t)base[x] + cnt[x], cap);
-    queue[x] = (int32_t)max((int64_t)0, end - base[x]);   // n
+    queue[x] = overflow ? 0 : (int32_t)max((int64_t)0, end - base[x]);   // n
     queue[8 + x] = base[x];                              // offset
     queue[16 + x] = 0;                                   // counter
+    if (x == 0) queue[QUEUE_OVERFLOW] = overflow ? 1 : 0;
   }
+  if (overflow) return;
   // each source's first item: the segment's fill plus the items of the
   // segment's earlier sources, by one scan per segment over each round of
   // 1024 sources (sources keep their order within a segment)
@@ -575,7 +585,8 @@ int64_t sbsa_prefill_items_bound(int64_t nnz, int num_queries, int num_kv_heads,
 int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clusters,
                        int num_queries, int queries_per_item, int has_local,
                        const int32_t* indptr, const int32_t* nvis, const int32_t* rev_indptr,
-                       void* items, int64_t items_cap, int32_t* queue, hipStream_t stream) {
+                       void* items, int64_t items_cap, int64_t partials_cap, int32_t* queue,
+                       hipStream_t stream) {
   if (!rev_counts || !items || !queue || queries_per_item < 1) return SBSA_ERR_ARG;
   if (!indptr || !nvis || !rev_indptr) return SBSA_ERR_ARG;
   const int nloc = has_local ? (num_queries + queries_per_item - 1) / queries_per_item : 0;
@@ -591,7 +602,7 @@ int sbsa_prefill_items(const int32_t* rev_counts, int num_kv_heads, int num_clus
   hipLaunchKernelGGL(build_items_kernel, dim3(1), dim3(1024), lds, stream, rev_counts, num_kv_heads,
                      num_clusters, num_queries, queries_per_item, has_local, indptr, nvis, rev_indptr,
                      (PrefillItem*)items, queue,
-                     items_cap);
+                     items_cap, partials_cap);
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }

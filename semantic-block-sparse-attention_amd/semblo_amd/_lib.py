@@ -39,12 +39,12 @@ SIGNATURES = {
     "sbsa_causal_sizes": (I32, [P, I64, P, P, I32, I32, I64, P, P]),
     "sbsa_reverse_index": (I32, [P, I32, I32, I32, P, P, P, P, P, I64, P, P]),
     "sbsa_prefill_items_bound": (I64, [I64, I32, I32, I32, I32]),
-    "sbsa_prefill_items": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, I64, P, P]),
+    "sbsa_prefill_items": (I32, [P, I32, I32, I32, I32, I32, P, P, P, P, I64, I64, P, P]),
     "sbsa_prefill_item_rows": (I32, []),
     "sbsa_prefill_attend": (I32, [P, I64, I64, I32, I32, I32, I32, P, I64, P, P, I64, I64, P, P,
                                   I32, P, P, P, P, P, P, P, I64, I64, P, I64, I64, F32, I32, P]),
     "sbsa_prefill_combine": (I32, [P, P, P, P, P, P, P, I64, I64, P, P, I64, I64, P, I32, I32,
-                                   I32, I32, I32, P]),
+                                   I32, I32, I32, P, P]),
     "sbsa_decode_workspace_bytes": (SZ, [I32, I32, I32, I32, I32, I32]),
     "sbsa_decode_step": (I32, [P, I64, P, I64, I32, P, P, I64, P, P, P, P, P, I64, P, I64, I32, P, I64,
                                I32, I32, I32, I32, I32, F32, F32, F32, I32, I32, F32, I32, I32, P,

@@ -138,10 +138,11 @@ def fused_chunk_plan(q_chunk: torch.Tensor, query_state, index, snapshot_state, 
 
 def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int | None = None, *,
                         sm_scale: float, fa3_page_size: int = 16, out: torch.Tensor | None = None,
-                        timing=None, window_kv=None) -> torch.Tensor:
+                        timing=None, window_kv=None, guard=None) -> torch.Tensor:
     """The attention of a planned sparse chunk.  ``nnz`` (its partial count, read on the
-    host) sizes the partial rows exactly; None sizes them by the capacity bound, so
-    the chunk is enqueued without waiting for its plan (kv_outer_execute)."""
+    host) sizes the partial rows exactly; None sizes them by the capacity bound, capped
+    in bytes, so the chunk is enqueued without waiting for its plan (kv_outer_execute;
+    ``guard``, a kv_outer.PartialsGuard, then settles a capped chunk later)."""
     q_count, hq, d = q_chunk.shape
     hkv = index.num_kv_heads
     wstart, chunk_start, chunk_end = plan.wstart, plan.chunk_start, plan.chunk_end
@@ -163,7 +164,7 @@ def fused_chunk_execute(plan: ChunkPlan, q_chunk: torch.Tensor, index, nnz: int 
         window = (k_orig[wstart:chunk_end + 1], v_orig[wstart:chunk_end + 1])
     res, _ = kv_outer_execute(q_chunk, index.packed_kv, plan.kv, nnz, index.bucket_indptr,
                               sm_scale=sm_scale, local_kv=window, chunk_start=chunk_start,
-                              wstart=wstart, out=out, timing=timing)
+                              wstart=wstart, out=out, timing=timing, guard=guard)
     return res
 
 
@@ -174,7 +175,7 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
                           fa3_page_size: int = 16, kv_outer_default: bool = True,
                           dense_prefix_x: int = 4, local: int = 0, out: torch.Tensor | None = None,
                           timing=None, window_kv=None, plan_log: list | None = None,
-                          **unused) -> torch.Tensor:
+                          guard=None, **unused) -> torch.Tensor:
     """Attention of one query chunk [chunk_start, chunk_end] (fused_prefill.py:219-482).
 
     While chunk_start <= dense_prefix_x * K the chunk is dense and causal over
@@ -184,7 +185,9 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     rows wstart..chunk_end in prompt order, replaces the slice of
     ``index.original_kv`` for that window (the token-order prefill, whose
     store has no prompt-order copy).  One host read (the partial count).
-    ``plan_log``: a test hook, see ChunkPlan.record.
+    ``plan_log``: a test hook, see ChunkPlan.record.  ``guard``: a kv_outer.PartialsGuard
+    that settles the chunk later if its partial rows were capped (with none, a capped
+    chunk is settled before returning: one host read).
     """
     if not kv_outer_default or not fa3_page_size:
         raise NotImplementedError("only the paper path (FA3 page body, KV-outer) is built")
@@ -211,7 +214,7 @@ def fused_chunk_attention(q_chunk: torch.Tensor, query_state, index, q_positions
     # no host read: the partial rows are sized by the capacity bound
     return fused_chunk_execute(plan, q_chunk, index, None, sm_scale=sm_scale,
                                fa3_page_size=fa3_page_size, out=out, timing=timing,
-                               window_kv=window_kv)
+                               window_kv=window_kv, guard=guard)
 
 
 def fused_decode_attention(q_chunk: torch.Tensor, query_state, index, q_positions: torch.Tensor, *,

@@ -14,9 +14,12 @@ log-sum-exp.  Here the same three steps are three libsbsa calls:
   sbsa_prefill_combine  window first, then the clusters in order (kv_outer.py:370-479)
 
 One host read per call (the entry count, which sizes the partial buffer), as
-in the reference (kv_outer.py:604-613).
+in the reference (kv_outer.py:604-613), or none: the partial rows are then
+sized by a bound known on the host, capped in bytes (PartialsGuard).
 """
 from __future__ import annotations
+
+import os
 
 import torch
 
@@ -115,6 +118,12 @@ def kv_outer_plan(qmask: torch.Tensor, causal_sizes: torch.Tensor, *, num_querie
     return KVOuterPlan(qmask, nvis, qvals, counts, rev_indptr, nnz_d, qrank)
 
 
+# int32 words of a work queue: per-XCD counts, offsets and counters, then the
+# overflow flag (word QUEUE_OVERFLOW)
+QUEUE_INTS = 32
+QUEUE_OVERFLOW = 24
+
+
 def partials_capacity(num_queries: int, num_kv_heads: int, num_clusters: int) -> int:
     """A bound of a chunk's partial count known without reading the device: a query
     selects at most every cluster of each KV head (one partial per selected,
@@ -122,14 +131,65 @@ def partials_capacity(num_queries: int, num_kv_heads: int, num_clusters: int) ->
     return int(num_queries) * int(num_kv_heads) * int(num_clusters)
 
 
+def partials_cap_bytes() -> int:
+    """SEMBLO_KV_OUTER_PARTIALS_CAP_MB (default 4096): the most bytes of partial rows a
+    chunk enqueued without a host read may take.  Past it the rows are sized to this
+    cap, and a chunk with more entries is run again at its exact count (the reference
+    caps its index buffers the same way and reads the count above the cap,
+    kv_outer.py:592-600)."""
+    return int(float(os.environ.get("SEMBLO_KV_OUTER_PARTIALS_CAP_MB", "4096")) * (1 << 20))
+
+
+class PartialsGuard:
+    """The chunks enqueued with a capped partial buffer, each with its overflow flag.
+
+    ``watch`` copies a chunk's flag to pinned memory behind its work (no wait);
+    ``poll`` settles the chunks whose flag has arrived, ``finish`` waits for the rest.
+    A chunk that overflowed ran nothing (its work list was empty and its combine
+    skipped): it is run again with its exact partial count, read on the host, and the
+    guard's later chunks get room for 1.25 times that count (``cap_entries``), since
+    the counts grow along a prompt."""
+
+    def __init__(self):
+        self._pending = []
+        self.reruns = 0
+        self.cap_entries = 0
+
+    def watch(self, queue: torch.Tensor, rerun) -> None:
+        flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        flag.copy_(queue[QUEUE_OVERFLOW:QUEUE_OVERFLOW + 1], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._pending.append((ev, flag, rerun))
+
+    def poll(self, wait: bool = False) -> None:
+        keep = []
+        for ev, flag, rerun in self._pending:
+            if wait:
+                ev.synchronize()
+            elif not ev.query():
+                keep.append((ev, flag, rerun))
+                continue
+            if int(flag[0]):
+                self.reruns += 1
+                rerun()
+        self._pending = keep
+
+    def finish(self) -> None:
+        self.poll(wait=True)
+
+
 def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan, nnz: int | None,
                      bucket_indptr: torch.Tensor, *, sm_scale: float, local_kv, chunk_start: int,
                      wstart: int, out: torch.Tensor | None = None, want_stats: bool = False,
-                     grid: int | None = None, timing=None):
+                     grid: int | None = None, timing=None, guard: PartialsGuard | None = None):
     """The work list, the attention and the combine of one chunk, given its plan and
     its partial count ``nnz`` read on the host, or None: the partial rows are then
-    sized by ``partials_capacity`` and nothing waits for the plan on the host (the
-    kernels take the count and the entries from the plan's device arrays)."""
+    sized by ``partials_capacity``, capped at ``partials_cap_bytes``, and nothing
+    waits for the plan on the host (the kernels take the count and the entries from
+    the plan's device arrays).  A capped chunk is settled through ``guard`` (its
+    overflow flag is read later, and the chunk run again if it overflowed), or, with
+    no guard, at once (one host read)."""
     qn, hq, d = q.shape
     hkv = packed_kv.shape[2]
     g = hq // hkv
@@ -138,7 +198,19 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     c = qmask.shape[2] * 32
     dev = q.device
     k_loc, v_loc = local_kv
-    cap = nnz if nnz is not None else partials_capacity(qn, hkv, c)
+    capped = False
+    if nnz is not None:
+        cap = nnz
+    else:
+        cap = partials_capacity(qn, hkv, c)
+        entry_bytes = g * d * q.element_size() + g * 4
+        limit = max(1, partials_cap_bytes() // entry_bytes)
+        if guard is not None:
+            limit = max(limit, guard.cap_entries)
+        if cap > limit:
+            cap, capped = limit, True
+    if out is None:
+        out = torch.empty_like(q)
     part_o = torch.empty(max(cap, 1), g, d, dtype=q.dtype, device=dev)
     part_lse = torch.empty(max(cap, 1), g, dtype=torch.float32, device=dev)
     local_o = torch.empty_like(q)
@@ -146,10 +218,11 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     qt = queries_per_item(g)
     bound = _lib.query("sbsa_prefill_items_bound", cap, qn, hkv, c, qt)
     items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
-    queue = torch.empty(24, dtype=torch.int32, device=dev)
+    queue = torch.empty(QUEUE_INTS, dtype=torch.int32, device=dev)
     s = _lib.stream(dev)
     _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
-              _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, _lib.ptr(queue), s)
+              _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, cap if capped else 0,
+              _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s, "sparse")
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,
@@ -161,12 +234,23 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
               int(wstart), float(sm_scale), int(grid or 0), s)
     if timing is not None:
         timing.end(s)
-    if out is None:
-        out = torch.empty_like(q)
     _lib.call("sbsa_prefill_combine", _lib.ptr(qmask), _lib.ptr(nvis), _lib.ptr(rev_indptr),
               _lib.ptr(qrank), _lib.ptr(part_o), _lib.ptr(part_lse), _lib.ptr(local_o),
               local_o.stride(0), local_o.stride(1), _lib.ptr(local_lse), _lib.ptr(out),
-              out.stride(0), out.stride(1), None, qn, hq, hkv, d, c, s)
+              out.stride(0), out.stride(1), None, qn, hq, hkv, d, c,
+              _lib.ptr(queue[QUEUE_OVERFLOW:]) if capped else None, s)
+    if capped:
+        def rerun():
+            exact = int(plan.nnz_d.item())
+            if guard is not None:
+                guard.cap_entries = max(guard.cap_entries, exact + exact // 4)
+            kv_outer_execute(q, packed_kv, plan, exact, bucket_indptr,
+                             sm_scale=sm_scale, local_kv=local_kv, chunk_start=chunk_start,
+                             wstart=wstart, out=out, grid=grid, timing=timing)
+        if guard is not None:
+            guard.watch(queue, rerun)
+        elif int(queue[QUEUE_OVERFLOW].item()):
+            rerun()
     stats = {"partials": nnz}
     if want_stats:
         stats["charged"] = int((counts.to(torch.int64) * nvis.to(torch.int64)).sum())
@@ -190,13 +274,13 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
     bound = hkv * ((qn + qt - 1) // qt) + 1
     items = torch.empty(bound, ITEM_INTS, dtype=torch.int32, device=dev)
-    queue = torch.empty(24, dtype=torch.int32, device=dev)
+    queue = torch.empty(QUEUE_INTS, dtype=torch.int32, device=dev)
     if out is None:
         out = torch.empty_like(q)
     s = _lib.stream(dev)
     # no cluster has queries: the index arrays are never read
     _lib.call("sbsa_prefill_items", _lib.ptr(zero_counts), hkv, 32, qn, qt, 1, _lib.ptr(zero_counts),
-              _lib.ptr(zero_counts), _lib.ptr(zero_counts), _lib.ptr(items), bound, _lib.ptr(queue), s)
+              _lib.ptr(zero_counts), _lib.ptr(zero_counts), _lib.ptr(items), bound, 0, _lib.ptr(queue), s)
     if timing is not None:
         timing.begin(s, "dense")
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,

@@ -24,6 +24,7 @@ from .attention_op import register_layer
 from .config import SembloRuntimeConfig
 from .fused_decode import fused_decode_step
 from .fused_prefill import CausalSnapshot, fused_chunk_execute, fused_chunk_plan
+from .kv_outer import PartialsGuard
 from .kv_outer import dense_causal_attention
 from .state import ProductPostingIndex
 from .trivial_router import trivial_router_vectors
@@ -214,6 +215,9 @@ class SembloAttention:
             ready.append(ev)
 
         self.index = index
+        # chunks whose partial rows were capped (kv_outer.partials_cap_bytes) are checked
+        # once, after the last chunk, and any that overflowed is run again
+        guard = PartialsGuard()
         for i in range(len(sparse)):
             enqueue_plan(i)
         for i, (st, en) in enumerate(sparse):
@@ -226,7 +230,9 @@ class SembloAttention:
             for t in pl.tensors():
                 t.record_stream(main)
             fused_chunk_execute(pl, q[st:en], index, None,
-                                sm_scale=self.scaling, out=out[st:en], timing=timing)
+                                sm_scale=self.scaling, out=out[st:en], timing=timing, guard=guard)
+        guard.finish()
+        self.partials_reruns = guard.reruns
         built = torch.cuda.Event()
         built.record(side)
         # the decode state uses the index on this stream

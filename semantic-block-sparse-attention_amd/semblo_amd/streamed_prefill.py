@@ -27,7 +27,7 @@ import torch
 
 from . import _lib
 from .fused_prefill import CausalSnapshot, chunk_window_start, fused_chunk_attention
-from .kv_outer import dense_causal_attention
+from .kv_outer import PartialsGuard, dense_causal_attention
 from .token_outer_prefill import gather_rows
 
 
@@ -107,6 +107,8 @@ class StreamedPrefillSession:
         o = out.view(n, hq, d)
         # a fresh snapshot per call, as the reference's loop makes one
         snapshot = CausalSnapshot(self.index)
+        # chunks whose partial rows were capped are settled once, before returning
+        guard = PartialsGuard()
         step = cfg.query_chunk_size
         for a in range(0, n, step):
             b = min(n, a + step)
@@ -127,7 +129,8 @@ class StreamedPrefillSession:
                                   beta=cfg.bucket_size_penalty, target_tokens=self.target,
                                   sm_scale=layer.scaling, iters=cfg.iters,
                                   dense_prefix_x=cfg.dense_prefix_x, out=o[a:b], timing=timing,
-                                  window_kv=window, plan_log=layer.plan_log)
+                                  window_kv=window, plan_log=layer.plan_log, guard=guard)
+        guard.finish()
         return out
 
     def finish(self):

@@ -43,7 +43,7 @@ import torch
 
 from . import _lib
 from .config import num_flat_clusters
-from .kv_outer import dense_causal_attention
+from .kv_outer import PartialsGuard, dense_causal_attention
 from .state import PACK_ALIGN, ProductPostingIndex
 
 
@@ -178,6 +178,7 @@ class TokenOuterPrefillSession:
         self._reserve_dev: torch.Tensor | None = None
         self.repacks = 0
         self.repacks_with_slice = 0                 # repacks whose layout counts the slice's keys
+        self.guard = PartialsGuard()                # sparse slices whose partial rows were capped
         self.next_start = 0
         self._spare: torch.Tensor | None = None     # the other buffer of the store, after a repack
         self._host: torch.Tensor | None = None      # pinned: the append's flags, counts and sizes
@@ -243,6 +244,7 @@ class TokenOuterPrefillSession:
             # the prompt ended before the fit point: fit on all of it
             self.fit_at = self.tokens
             self._fit_and_pack()
+        self.guard.finish()
         self._spare = None
         self.layer.adopt_index(self.index)
         return self.index
@@ -340,6 +342,8 @@ class TokenOuterPrefillSession:
         s = _lib.stream(kk.device)
         ids, rows, counts = pending["ids"], pending["rows"], pending["counts"]
         pending["ready"].synchronize()
+        # capped chunks whose overflow flags have arrived (no wait)
+        self.guard.poll()
         host = self._host
         flags_h = host[:hkv]
         if bool((flags_h & 2).any()):
@@ -358,6 +362,9 @@ class TokenOuterPrefillSession:
                 # always fits; the reference's intermediate layout is skipped.
                 reserve = reserved_layout(sizes_h + counts_h, start + n, self.tokens, width, align)
                 self.repacks_with_slice += 1
+            # a capped chunk run again reads the store as its plan saw it: settle every
+            # such chunk before the runs move
+            self.guard.finish()
             self._repack(start, reserve)
             rows, counts, _ = append_rows(ids, index.bucket_indptr, index.bucket_sizes, None)
         if kk.stride() != vv.stride() or kk.stride(-1) != 1:
@@ -428,4 +435,4 @@ class TokenOuterPrefillSession:
                               temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
                               target_tokens=self.target, sm_scale=layer.scaling, iters=cfg.iters,
                               dense_prefix_x=cfg.dense_prefix_x, out=out, timing=timing,
-                              window_kv=(kk, vv), plan_log=layer.plan_log)
+                              window_kv=(kk, vv), plan_log=layer.plan_log, guard=self.guard)

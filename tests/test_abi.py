@@ -83,7 +83,7 @@ def test_entry_points_reject_bad_arguments_before_any_launch():
     assert need == 64 * 32 * 4
     assert lib.sbsa_kmeans_update(p, 256, p, 1000, p, 64, 256, p, p, p, need - 1, None) == 4
     # the work list without the reverse index's arrays
-    assert lib.sbsa_prefill_items(p, 4, 64, 128, 32, 1, None, p, p, p, 100, p, None) == 1
+    assert lib.sbsa_prefill_items(p, 4, 64, 128, 32, 1, None, p, p, p, 100, 0, p, None) == 1
     # a window that starts after the chunk
     assert lib.sbsa_prefill_attend(p, 4096, 256, 128, 16, 4, 256, p, 1024, p, p, 1024, 256, p, p,
                                    64, p, p, p, p, p, p, p, 4096, 256, p, 512, 1024, 0.0625, 0,
