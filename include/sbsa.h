@@ -241,7 +241,13 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
  * vectors already (router_pass 0).  pos is a device int.  The suffix holds at
  * most 16*max_tiles positions from prompt_len (max_tiles 0: no suffix), and
  * table maps logical blocks prompt_len/suffix_block through
- * (prompt_len + 16*max_tiles - 1)/suffix_block.  num_splits + suffix_splits
+ * (prompt_len + 16*max_tiles - 1)/suffix_block.  prompt_len_dev (optional,
+ * int32 [1]): the prompt length read on the device instead of prompt_len, so
+ * that a captured step follows a suffix flush (the arena's prompt_length_t,
+ * semblo/vllm_plugin/arena.py:118-124, suffix_flush.py:230).  kpre_new /
+ * suffix_kpre (optional, [Hkv, dim] at kn_sh / [suffix_nblk, suffix_block,
+ * Hkv, dim]): the token's pre-RoPE key is stored beside its K/V, for the
+ * flush's routing (arena.py:138-141).  num_splits + suffix_splits
  * <= 512.  No host reads, no allocation: capturable in a HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
  * then rcount [Hkv] and rtokens [Hkv]; of each head's C entries only the first
  * rcount[h] are written by the step (the rest keep earlier contents). */
@@ -252,6 +258,7 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      const void* codebooks, const int32_t* sizes, const int32_t* indptr,
                      const void* packed, int64_t packed_len, void* suffix_kv, int64_t suffix_nblk,
                      int suffix_block, const int32_t* table, int64_t prompt_len, int max_tiles,
+                     const int32_t* prompt_len_dev, const void* kpre_new, void* suffix_kpre,
                      int num_q_heads, int num_kv_heads, int num_clusters, int dim,
                      float inv_temperature, float beta, float target_tokens, int iters,
                      int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
@@ -276,7 +283,9 @@ int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre
                              const int32_t* indptr, const void* packed, int64_t packed_len,
                              void* suffix_kv, int64_t suffix_nblk, int suffix_block,
                              const int32_t* table, int64_t prompt_len, int max_tiles,
-                             int num_q_heads, int num_kv_heads, int num_clusters, int dim,
+                             const int32_t* prompt_len_dev, const void* kpre_new,
+                             void* suffix_kpre, int num_q_heads, int num_kv_heads,
+                             int num_clusters, int dim,
                              float inv_temperature, float beta, float target_tokens, int iters,
                              int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
                              void* out, int64_t out_sh, float* out_lse, int32_t* csr_out,

@@ -659,3 +659,47 @@ def relayout_rows(old_rows: torch.Tensor, old_indptr: torch.Tensor,
         b = torch.searchsorted(ip, r, right=True) - 1
         out[h] = r - ip[b] + new_indptr[h].to(torch.int64)[b]
     return out
+
+
+# ------------------------------------------------------------ suffix flush -----
+
+def flush_range(prompt_len: int, written: int, plen_cur: int, keep: int, every: int):
+    """suffix_flush.py:140-152: the positions [frm, to) to move, or None.  ``written``
+    generated tokens sit at [prompt_len, prompt_len + written); those below ``plen_cur``
+    were moved already.  Once keep + every tokens are exact, all but the newest keep move."""
+    live = prompt_len + written - plen_cur
+    if live >= keep + every:
+        return plen_cur, prompt_len + written - keep
+    return None
+
+
+def flush_store(posting: torch.Tensor, indptr: torch.Tensor, sizes: torch.Tensor,
+                ids: torch.Tensor, first_position: int, align: int):
+    """The layout after a flush (repack_plan / repack_apply, suffix_flush.py:55-137).
+
+    posting [Hkv, W], indptr [Hkv, C+1], sizes [Hkv, C] of the store before; ids [Hkv, n]
+    the clusters of positions first_position .. first_position + n - 1.  Every cluster
+    keeps its rows in order and takes its newcomers after them in position order; the
+    runs are laid out again from row 0, each padded to a whole number of ``align`` rows.
+    Returns (runs, new_sizes [Hkv, C], new_indptr [Hkv, C+1]) with runs[h][c] the
+    positions of cluster c's rows in row order."""
+    hkv, c = sizes.shape
+    align = max(int(align), 1)
+    runs = []
+    new_sizes = torch.zeros(hkv, c, dtype=torch.int64)
+    new_indptr = torch.zeros(hkv, c + 1, dtype=torch.int64)
+    for h in range(hkv):
+        lists = []
+        for b in range(c):
+            st = int(indptr[h, b])
+            lists.append([int(x) for x in posting[h, st:st + int(sizes[h, b])].tolist()])
+        for i, b in enumerate(ids[h].tolist()):
+            lists[b].append(int(first_position) + i)
+        runs.append(lists)
+        row = 0
+        for b in range(c):
+            new_sizes[h, b] = len(lists[b])
+            new_indptr[h, b] = row
+            row += -(-len(lists[b]) // align) * align
+        new_indptr[h, c] = row
+    return runs, new_sizes, new_indptr

@@ -49,6 +49,9 @@ struct DecodeArgs {
   int BS;
   const int32_t* table;     // logical block -> physical block
   int64_t prompt_len;
+  const int32_t* plen_dev;  // [1] the prompt length on the device (overrides prompt_len), or null
+  const bf16_t* kpre_new;   // [Hkv, D] pre-RoPE key rows at kn_sh, or null
+  bf16_t* suffix_kpre;      // [NBLK, BS, Hkv, D], or null (no pre-RoPE suffix store)
   int32_t* rstart;          // [Hkv, C]
   int32_t* rlen;
   int32_t* rcum;
@@ -102,7 +105,7 @@ size_t step_lds_bytes(int G, int C) {
 // the CSR of the head's selection in s_rstart / s_rcum (rcount entries) and
 // s_cnt = {rcount, rtokens}.
 template <int D, int NK, typename Prefetch>
-__device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, int pos_v,
+__device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, int pos_v, int64_t plen,
                                              Prefetch prefetch, unsigned char* smem, int* s_rstart,
                                              int* s_rcum, int* s_cnt) {
   constexpr int KS = D / 32;
@@ -223,16 +226,20 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     // the token's K/V into the suffix store, once per head (a position past
     // the reservation is not written: the table does not cover it)
     const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
-    if (leader && a.k_new && q_pos >= a.prompt_len && q_pos - a.prompt_len < (int64_t)a.max_tiles * 16) {
+    if (leader && a.k_new && q_pos >= plen && q_pos - plen < (int64_t)a.max_tiles * 16) {
       const int64_t blk = q_pos / a.BS;
       const int64_t off = q_pos - blk * a.BS;
       const int64_t phys = a.table[blk];
       const int64_t plane = a.suffix_nblk * a.BS * a.Hkv * D;
-      bf16_t* dst = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
+      const int64_t at = ((phys * a.BS + off) * a.Hkv + h) * D;
+      bf16_t* dst = a.suffix_kv + at;
       for (int d = threadIdx.x - 64; d < D; d += 192) {
         dst[d] = a.k_new[(int64_t)h * a.kn_sh + d];
         dst[plane + d] = a.v_new[(int64_t)h * a.kn_sh + d];
       }
+      // the pre-RoPE key too, for a later move of the token into the clusters
+      if (a.suffix_kpre && a.kpre_new)
+        for (int d = threadIdx.x - 64; d < D; d += 192) a.suffix_kpre[at + d] = a.kpre_new[(int64_t)h * a.kn_sh + d];
     }
   } else {
     // 4. bisection and the CSR (wave 0); sizes are integers below 2^24, so
@@ -366,9 +373,15 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
   // the position as a vector load (a scalar load would be waited on by the
   // first LDS access)
   const int pos_v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the prompt length: tokens moved into the clusters after the prefill raise
+  // it on the device, so a captured step reads it there
+  const int64_t plen = a.plen_dev
+      ? (int64_t)__builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(a.plen_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      : a.prompt_len;
   // suffix block table entries the live suffix may use (at most MAX_TABLE)
-  const int64_t tb0 = a.prompt_len / a.BS;
-  const int64_t tb_n = a.max_tiles > 0 ? (a.prompt_len + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
+  const int64_t tb0 = plen / a.BS;
+  const int64_t tb_n = a.max_tiles > 0 ? (plen + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
   const bool table_in_lds = tb_n <= MAX_TABLE;
   if (table_in_lds && wave == 0)   // copied straight into LDS; waited on in the selection
     for (int k = 0; k * 64 < tb_n; ++k)
@@ -387,13 +400,13 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
       qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
   };
 
-  select_phase<D, NK>(a, h, split == 0, pos_v, load_q, smem_dec, s_rstart, s_rcum, s_cnt);
+  select_phase<D, NK>(a, h, split == 0, pos_v, plen, load_q, smem_dec, s_rstart, s_rcum, s_cnt);
   const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
 
   // this split's range of the head's key list (prompt rows, then suffix rows)
   const int rcount = s_cnt[0];
   const int count = s_cnt[1];
-  int64_t nsuf64 = q_pos - a.prompt_len + 1;
+  int64_t nsuf64 = q_pos - plen + 1;
   nsuf64 = nsuf64 < 0 ? 0 : (nsuf64 > (int64_t)a.max_tiles * 16 ? (int64_t)a.max_tiles * 16 : nsuf64);
   const int total = count + (int)nsuf64;
   const int per = ((total + S - 1) / S + DT - 1) / DT * DT;
@@ -440,7 +453,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
           kp = a.packed + (row * a.Hkv + h) * D;
           vp = kp + pplane;
         } else {
-          const int64_t p = a.prompt_len + (oo - count);
+          const int64_t p = plen + (oo - count);
           if (a.k_new && p == q_pos) {
             kp = a.k_new + (int64_t)h * a.kn_sh;
             vp = a.v_new + (int64_t)h * a.kn_sh;
@@ -676,7 +689,8 @@ int decode_step_impl(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      const int32_t* pos, const void* codebooks, const int32_t* sizes,
                      const int32_t* indptr, const void* packed, int64_t packed_len,
                      void* suffix_kv, int64_t suffix_nblk, int suffix_block, const int32_t* table,
-                     int64_t prompt_len, int max_tiles, int num_q_heads, int num_kv_heads,
+                     int64_t prompt_len, int max_tiles, const int32_t* prompt_len_dev,
+                     const void* kpre_new, void* suffix_kpre, int num_q_heads, int num_kv_heads,
                      int num_clusters, int dim, float inv_temperature, float beta,
                      float target_tokens, int iters, int sink_tokens, float sm_scale,
                      int num_splits, int suffix_splits, void* workspace, size_t workspace_bytes,
@@ -719,6 +733,9 @@ int decode_step_impl(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   a.BS = suffix_block;
   a.table = table;
   a.prompt_len = prompt_len;
+  a.plen_dev = prompt_len_dev;
+  a.kpre_new = (const bf16_t*)kpre_new;
+  a.suffix_kpre = (bf16_t*)suffix_kpre;
   int32_t* w = (int32_t*)workspace;
   a.rstart = w;
   a.rlen = w + num_kv_heads * C;
@@ -794,7 +811,8 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      const int32_t* pos, const void* codebooks, const int32_t* sizes,
                      const int32_t* indptr, const void* packed, int64_t packed_len,
                      void* suffix_kv, int64_t suffix_nblk, int suffix_block, const int32_t* table,
-                     int64_t prompt_len, int max_tiles, int num_q_heads, int num_kv_heads,
+                     int64_t prompt_len, int max_tiles, const int32_t* prompt_len_dev,
+                     const void* kpre_new, void* suffix_kpre, int num_q_heads, int num_kv_heads,
                      int num_clusters, int dim, float inv_temperature, float beta,
                      float target_tokens, int iters, int sink_tokens, float sm_scale,
                      int num_splits, int suffix_splits, void* workspace, size_t workspace_bytes,
@@ -802,7 +820,8 @@ int sbsa_decode_step(const void* q_post, int64_t q_sh, const void* q_pre, int64_
                      hipStream_t stream) {
   return decode_step_impl(q_post, q_sh, q_pre, qp_sh, router_pass, k_new, v_new, kn_sh, pos,
                           codebooks, sizes, indptr, packed, packed_len, suffix_kv, suffix_nblk,
-                          suffix_block, table, prompt_len, max_tiles, num_q_heads, num_kv_heads,
+                          suffix_block, table, prompt_len, max_tiles, prompt_len_dev, kpre_new,
+                          suffix_kpre, num_q_heads, num_kv_heads,
                           num_clusters, dim, inv_temperature, beta, target_tokens, iters,
                           sink_tokens, sm_scale, num_splits, suffix_splits, workspace,
                           workspace_bytes, out, out_sh, out_lse, csr_out, stream);
@@ -816,7 +835,9 @@ int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre
                              const int32_t* indptr, const void* packed, int64_t packed_len,
                              void* suffix_kv, int64_t suffix_nblk, int suffix_block,
                              const int32_t* table, int64_t prompt_len, int max_tiles,
-                             int num_q_heads, int num_kv_heads, int num_clusters, int dim,
+                             const int32_t* prompt_len_dev, const void* kpre_new,
+                             void* suffix_kpre, int num_q_heads, int num_kv_heads,
+                             int num_clusters, int dim,
                              float inv_temperature, float beta, float target_tokens, int iters,
                              int sink_tokens, float sm_scale, int num_splits, int suffix_splits,
                              void* out, int64_t out_sh, float* out_lse, int32_t* csr_out,
@@ -831,7 +852,8 @@ int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre
   if (!ws) return SBSA_ERR_LAUNCH;
   return decode_step_impl(q_post, q_sh, q_pre, qp_sh, router_pass, k_new, v_new, kn_sh, pos,
                           codebooks, sizes, indptr, packed, packed_len, suffix_kv, suffix_nblk,
-                          suffix_block, table, prompt_len, max_tiles, num_q_heads, num_kv_heads,
+                          suffix_block, table, prompt_len, max_tiles, prompt_len_dev, kpre_new,
+                          suffix_kpre, num_q_heads, num_kv_heads,
                           num_clusters, dim, inv_temperature, beta, target_tokens, iters,
                           sink_tokens, sm_scale, num_splits, suffix_splits, ws, need, out,
                           out_sh, out_lse, csr_out, stream);

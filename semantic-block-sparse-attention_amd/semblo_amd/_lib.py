@@ -47,12 +47,12 @@ SIGNATURES = {
                                    I32, I32, I32, P, P]),
     "sbsa_decode_workspace_bytes": (SZ, [I32, I32, I32, I32, I32, I32]),
     "sbsa_decode_step": (I32, [P, I64, P, I64, I32, P, P, I64, P, P, P, P, P, I64, P, I64, I32, P, I64,
-                               I32, I32, I32, I32, I32, F32, F32, F32, I32, I32, F32, I32, I32, P,
-                               SZ, P, I64, P, P, P]),
+                               I32, P, P, P, I32, I32, I32, I32, F32, F32, F32, I32, I32, F32, I32,
+                               I32, P, SZ, P, I64, P, P, P]),
     "sbsa_decode_scratch_bytes": (SZ, []),
     "sbsa_decode_step_noalloc": (I32, [P, I64, P, I64, I32, P, P, I64, P, P, P, P, P, I64, P, I64,
-                                       I32, P, I64, I32, I32, I32, I32, I32, F32, F32, F32, I32,
-                                       I32, F32, I32, I32, P, I64, P, P, P]),
+                                       I32, P, I64, I32, P, P, P, I32, I32, I32, I32, F32, F32,
+                                       F32, I32, I32, F32, I32, I32, P, I64, P, P, P]),
     "sbsa_nearest_cluster": (I32, [P, I64, I64, I64, I32, I32, I32, P, I32, P, P]),
     "sbsa_append_rows": (I32, [P, I64, I32, I32, P, P, P, P, P, P, P]),
     "sbsa_append_kv": (I32, [P, P, I64, I64, I64, I32, I32, P, I64, P, I64, P, I64, P, I64, P, P,

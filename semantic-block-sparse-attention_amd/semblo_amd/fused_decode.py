@@ -70,17 +70,24 @@ def fused_decode_step(layer, arena, *, q_post: torch.Tensor, q_pre: torch.Tensor
     pos = positions[:1]
     if pos.dtype != torch.int32:
         raise ValueError("positions must be int32 (converting would allocate inside a capture)")
-    kk = vv = None
+    kk = vv = kp = None
     if k_post is not None and v_states is not None:
         kk = k_post.reshape(hkv, d)
         vv = v_states.reshape(hkv, d)
+        if k_pre is not None and getattr(arena, "suffix_kpre", None) is not None:
+            kp = k_pre.reshape(hkv, d)
+            if kp.stride(0) != kk.stride(0) or kp.stride(-1) != 1:
+                raise ValueError("k_pre must share k_post's row layout (the step stores both)")
     out = output.reshape(hq, d)
     head = (_lib.ptr(q), q.stride(0), _lib.ptr(qp), qp.stride(0), 1,
             _lib.ptr(kk), _lib.ptr(vv), kk.stride(0) if kk is not None else 0, _lib.ptr(pos),
             _lib.ptr(arena.codebooks), _lib.ptr(arena.sizes), _lib.ptr(arena.indptr),
             _lib.ptr(arena.packed_kv), arena.packed_kv.shape[1], _lib.ptr(arena.suffix_kv),
             arena.suffix_kv.shape[1], arena.suffix_block, _lib.ptr(arena.suffix_table),
-            arena.prompt_length, arena.max_tiles, hq, hkv, c, d, 1.0 / float(temperature),
+            arena.prompt_length, arena.max_tiles,
+            _lib.ptr(arena.prompt_length_t) if arena.reads_prompt_length_on_device else None,
+            _lib.ptr(kp), _lib.ptr(arena.suffix_kpre) if kp is not None else None, hq, hkv, c, d,
+            1.0 / float(temperature),
             float(beta), float(target_tokens), int(iters), fitted_sink_tokens(), float(sm_scale),
             int(num_splits), ss)
     tail = (_lib.ptr(out), out.stride(0), _lib.ptr(out_lse), _lib.ptr(csr_out), _lib.stream(q.device))
@@ -130,7 +137,8 @@ def decode_prompt_only(q_chunk: torch.Tensor, vectors: torch.Tensor, index, *, t
     _lib.call("sbsa_decode_step", _lib.ptr(q), d, _lib.ptr(v), d, 0, None, None, 0, _lib.ptr(pos),
               _lib.ptr(holder.codebooks), _lib.ptr(holder.sizes), _lib.ptr(holder.indptr),
               _lib.ptr(holder.packed_kv), holder.packed_kv.shape[1], _lib.ptr(holder.suffix_kv), 1,
-              256, _lib.ptr(holder.suffix_table), holder.prompt_length, holder.max_tiles, hq, hkv,
+              256, _lib.ptr(holder.suffix_table), holder.prompt_length, holder.max_tiles, None, None,
+              None, hq, hkv,
               index.num_buckets, d, 1.0 / float(temperature), float(beta), float(target_tokens),
               int(iters), fitted_sink_tokens(), float(sm_scale), int(num_splits), 1,
               _lib.ptr(ws.buffer), ws.nbytes,

@@ -19,6 +19,7 @@ import os
 
 import torch
 
+from . import suffix_flush
 from .arena import DecodeArena
 from .attention_op import register_layer
 from .config import SembloRuntimeConfig
@@ -131,8 +132,15 @@ class SembloAttention:
         self.index = index
         shuffle = None if cfg.suffix_shuffle_seed is None else \
             torch.Generator().manual_seed(int(cfg.suffix_shuffle_seed))
+        every = suffix_flush.flush_every()
+        if every > 0 and suffix_flush.keep_exact() + every > cfg.suffix_reserve - 2 * cfg.suffix_block:
+            raise RuntimeError(
+                f"SEMBLO_SUFFIX_KEEP_EXACT + SEMBLO_SUFFIX_FLUSH_EVERY = "
+                f"{suffix_flush.keep_exact() + every} exact tokens do not fit the suffix store of "
+                f"{cfg.suffix_reserve} positions (suffix_reserve) less two blocks")
         self.arena = DecodeArena(index, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
-                                 suffix_splits=cfg.decode_suffix_splits, shuffle_blocks=shuffle)
+                                 suffix_splits=cfg.decode_suffix_splits, shuffle_blocks=shuffle,
+                                 flush_room=suffix_flush.flush_room() if every > 0 else 0)
 
     def prefill_token_order(self, q_post, q_pre, k_pre, k_post, v, output, chunk: int,
                             timing=None, store_timing=None, **kw) -> torch.Tensor:
@@ -245,19 +253,27 @@ class SembloAttention:
         return output
 
     # -- decode -----------------------------------------------------------------
-    def decode(self, positions, q_post, q_pre, k_post, v, output) -> torch.Tensor:
+    def decode(self, positions, q_post, q_pre, k_post, v, output, k_pre=None) -> torch.Tensor:
+        """One decode step.  ``k_pre`` (the token's pre-RoPE key) is kept for the suffix
+        flush, which routes the moved tokens; without the flush it is not read."""
         if self.arena is None:
             raise RuntimeError("decode before any prefill: the layer has no index")
         cfg = self.runtime_config
-        # The suffix store holds `reserve` generated positions (the reference sizes it to the
-        # model's room for generated tokens, arena.py:50-63); a step past it would neither
-        # store nor read its token, so it is refused here, counted on the host.
-        if self.arena.steps >= self.arena.reserve:
-            raise RuntimeError(f"the decode suffix holds {self.arena.reserve} generated positions "
+        arena = self.arena
+        if arena.flush_room:
+            # the suffix flush (SEMBLO_SUFFIX_FLUSH_EVERY), on the host before the step, as
+            # the reference's hook around execute_model (suffix_flush.py:264-302)
+            suffix_flush.maybe_flush(arena)
+        # The suffix store holds `reserve` generated positions past the prompt length (the
+        # reference sizes it to the model's room for generated tokens, arena.py:50-63); a
+        # step past it would neither store nor read its token, so it is refused here,
+        # counted on the host.
+        if arena.first_prompt_length + arena.steps - arena.prompt_length >= arena.reserve:
+            raise RuntimeError(f"the decode suffix holds {arena.reserve} generated positions "
                                f"(suffix_reserve); raise it to the generation length")
-        self.arena.steps += 1
+        arena.steps += 1
         fused_decode_step(self, self.arena, q_post=q_post, q_pre=q_pre, positions=positions,
-                          k_post=k_post, v_states=v, output=output,
+                          k_post=k_post, v_states=v, k_pre=k_pre, output=output,
                           temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
                           target_tokens=self.target_tokens, sm_scale=self.scaling,
                           num_splits=cfg.decode_num_splits, iters=cfg.iters,
@@ -277,4 +293,4 @@ class SembloAttention:
             pos = positions.reshape(-1)[:1]
             if pos.dtype != torch.int32:
                 pos = pos.to(torch.int32)
-            self.decode(pos, q_post, q_pre, k_post, v_states, output)
+            self.decode(pos, q_post, q_pre, k_post, v_states, output, k_pre=k_pre)

@@ -112,9 +112,9 @@ def test_combine_refuses_rows_that_are_not_16_byte_aligned():
     p = 256
     # G * D = 1024: 16-byte row pieces; an output row stride of 4 elements is refused
     assert lib.sbsa_prefill_combine(p, p, p, p, p, p, p, 4096, 256, p, p, 4, 256, None,
-                                    8, 16, 4, 256, 128, None) == 1
+                                    8, 16, 4, 256, 128, None, None) == 1
     assert lib.sbsa_prefill_combine(p, p, p, p, p, p, p, 4100, 256, p, p, 4096, 256, None,
-                                    8, 16, 4, 256, 128, None) == 1
+                                    8, 16, 4, 256, 128, None, None) == 1
 
 
 def test_decode_without_allocation_refuses_shapes_past_its_scratch():
@@ -130,5 +130,6 @@ def test_decode_without_allocation_refuses_shapes_past_its_scratch():
     # 64 query heads x 500 splits x 256 dims of fp32 partials: far past 8 MiB
     assert _lib.query("sbsa_decode_workspace_bytes", 64, 8, 1024, 256, 492, 8) > cap
     assert lib.sbsa_decode_step_noalloc(p, 256, p, 256, 1, None, None, 0, p, p, p, p, p, 1000, p,
-                                        4, 256, p, 1000, 4, 64, 8, 1024, 256, 10.0, 0.25, 100.0,
+                                        4, 256, p, 1000, 4, None, None, None, 64, 8, 1024, 256,
+                                        10.0, 0.25, 100.0,
                                         16, 0, 0.0625, 492, 8, p, 256, None, None, None) == 4

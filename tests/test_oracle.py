@@ -284,3 +284,77 @@ def test_sink_hold_out_and_forced_bit_known_answers():
     got = ref.unpack_bits(qmask, 64)
     assert got[..., 0].all()
     assert int(got[..., 1:].sum()) == 2
+
+
+def test_flush_range_keeps_the_exact_suffix_between_keep_and_keep_plus_every():
+    """suffix_flush.py:140-152: simulated over a long generation, the moved ranges are
+    contiguous from the prompt's end, and after each step's flush decision the exact
+    suffix holds fewer than keep + every tokens, at least keep once it first reached
+    keep + every, and exactly keep right after a move."""
+    prompt, keep, every = 1000, 48, 32
+    plen, moved = prompt, []
+    for written in range(400):
+        rng = ref.flush_range(prompt, written, plen, keep, every)
+        live = prompt + written - plen
+        if rng is not None:
+            frm, to = rng
+            assert frm == plen and to - frm >= every and live >= keep + every
+            moved.append(rng)
+            plen = to
+        live = prompt + written - plen
+        assert live < keep + every
+        if moved:
+            assert keep <= live
+            assert live == keep or rng is None
+    assert moved[0] == (prompt, prompt + every)
+    assert len(moved) == (399 - (keep + every)) // every + 1
+    assert all(a[1] == b[0] for a, b in zip(moved, moved[1:]))
+
+
+def test_flush_store_known_answer_and_invariants():
+    """The layout after a flush (suffix_flush.py:55-137) on a hand-worked case:
+    sizes [2, 0, 3] at align 4 with newcomers to clusters [2, 0, 2] -> sizes [3, 0, 5],
+    runs at rows 0, 4, 4 (the padded runs 4 + 0 + 8), each cluster's old rows then its
+    newcomers in position order; and, on random stores, no position lost or doubled."""
+    posting = torch.tensor([[7, 3, -1, -1, 1, 0, 9, -1]])
+    indptr = torch.tensor([[0, 4, 4, 8]])
+    sizes = torch.tensor([[2, 0, 3]])
+    ids = torch.tensor([[2, 0, 2]])
+    runs, new_sizes, new_indptr = ref.flush_store(posting, indptr, sizes, ids, 20, 4)
+    assert runs[0] == [[7, 3, 21], [], [1, 0, 9, 20, 22]]
+    assert new_sizes.tolist() == [[3, 0, 5]] and new_indptr.tolist() == [[0, 4, 4, 12]]
+    gen = torch.Generator().manual_seed(3)
+    for trial in range(20):
+        hkv, c, align = 2, 16, 16
+        n_old = int(torch.randint(1, 300, (1,), generator=gen))
+        n_new = int(torch.randint(0, 60, (1,), generator=gen))
+        post, ip, sz = [], [], []
+        for h in range(hkv):
+            assign = torch.randint(0, c, (n_old,), generator=gen)
+            perm = torch.randperm(n_old, generator=gen)
+            counts = torch.bincount(assign, minlength=c)
+            pad = (counts + align - 1) // align * align
+            ptr = torch.zeros(c + 1, dtype=torch.int64)
+            ptr[1:] = pad.cumsum(0)
+            row = torch.full((int(ptr[-1]) + 1,), -1, dtype=torch.int64)
+            fill = ptr[:-1].clone()
+            for p in perm.tolist():
+                row[fill[assign[p]]] = p
+                fill[assign[p]] += 1
+            post.append(row)
+            ip.append(ptr)
+            sz.append(counts)
+        width = max(int(x.numel()) for x in post)
+        posting = torch.stack([torch.cat([x, x.new_full((width - x.numel(),), -1)]) for x in post])
+        ids = torch.randint(0, c, (hkv, n_new), generator=gen)
+        runs, new_sizes, new_indptr = ref.flush_store(posting, torch.stack(ip), torch.stack(sz), ids,
+                                                      n_old, align)
+        for h in range(hkv):
+            flat = sorted(p for lst in runs[h] for p in lst)
+            assert flat == list(range(n_old + n_new))
+            assert (new_indptr[h] % align == 0).all()
+            assert (new_indptr[h, 1:] - new_indptr[h, :-1] >= new_sizes[h]).all()
+            for b in range(c):
+                old = posting[h, int(ip[h][b]):int(ip[h][b]) + int(sz[h][b])].tolist()
+                newc = [n_old + i for i in range(n_new) if int(ids[h, i]) == b]
+                assert runs[h][b] == old + newc
