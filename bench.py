@@ -61,7 +61,9 @@ def _parse():
                     help="splits per KV head of the decode step (default: the runtime config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-queries", type=int, default=64)
-    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--only", choices=["all", "prefill", "decode", "dense-alone"], default="all",
+                    help="dense-alone: the configuration's dense-prefix chunks by themselves, with no "
+                         "index build beside them (for the attention kernel's own counters)")
     ap.add_argument("--extra-configs", type=lambda t: [int(x) for x in t.split(",") if x],
                     default=[2, 4], help="further BASELINE configurations measured after the "
                     "headline one and reported under extra_keys (comma list; empty for none)")
@@ -545,6 +547,41 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
     return fields
 
 
+def dense_alone(args) -> dict:
+    """The dense-prefix chunks of a configuration on their own stream with nothing beside
+    them: exact causal attention of each chunk over every earlier position."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.kv_outer import KernelTiming, dense_causal_attention
+    from semblo_amd.synthetic import CONFIGS, mixture_layer
+    conf = CONFIGS[args.config]
+    hq, hkv, d, chunk = conf["hq"], conf["hkv"], conf["d"], conf["chunk"]
+    cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=chunk)
+    cap = cfg.dense_prefix_x * cfg.budget(conf["length"])
+    length = min(conf["length"], (cap // chunk + 1) * chunk)
+    inp = mixture_layer(length, hq, hkv, d, mixtures=conf["mixtures"], seg=conf["seg"],
+                        log_uniform=conf["log_uniform"], sinks=conf["sinks"], seed=0,
+                        dtype=torch.bfloat16, device="cuda")
+    out = torch.empty_like(inp.q)
+    timing = KernelTiming(counts_flops=False)
+    flops = 0.0
+    for rep in range(args.warmup + args.steps):
+        t = timing if rep >= args.warmup else None
+        for cs in range(0, length, chunk):
+            n = min(chunk, length - cs)
+            if rep == 0:
+                flops += 4.0 * d * hq * (n * (cs + 1) + n * (n - 1) // 2)
+            dense_causal_attention(inp.q[cs:cs + n], inp.k, inp.v, sm_scale=d ** -0.5, chunk_start=cs,
+                                   out=out[cs:cs + n], timing=t)
+    torch.cuda.synchronize()
+    ms = timing.total_ms() / max(args.steps, 1)
+    ach = flops / (ms * 1e-3) / 1e12
+    _log(f"dense-prefix chunks alone: {length // chunk} chunks, {ms:.2f} ms, {flops / 1e12:.2f} TFLOP "
+         f"-> {ach:.0f} TFLOP/s")
+    return {"metric": "dense-prefix chunks alone, ms per layer", "value": round(ms, 3), "unit": "ms",
+            "achieved_tflops": round(ach, 1), "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+            "config": {"workload": f"config {args.config}: positions 0..{length - 1}, chunk {chunk}"}}
+
+
 def main():
     args = _parse()
     if args.gpus != 1:
@@ -553,6 +590,9 @@ def main():
         sys.exit(2)
     import semblo_amd
     semblo_amd.load_library()
+    if args.only == "dense-alone":
+        print(json.dumps(dense_alone(args)), flush=True)
+        return
     head = measure(args, args.config, args.steps, args.warmup, with_cpu=True)
     if args.copy_calibration:
         src = torch.empty(1 << 29, dtype=torch.int16, device="cuda").fill_(1)
