@@ -41,9 +41,33 @@ struct AttnArgs {
   int64_t lo_sq, lo_sh;
   float* local_lse;         // [Qc, Hq] or null
   int Hkv, C, Hq;
+  int Qc;                   // queries of the chunk
   int64_t chunk_start, wstart;
   float scale_log2;         // sm_scale * log2(e)
+#ifdef SBSA_ATTN_PROBE
+  int probe_slot;
+#endif
 };
+
+#ifdef SBSA_ATTN_PROBE
+// timing probe (a build flag, not in the product): per launch slot and block,
+// the wall clock at each item start, tagged with the item
+struct ProbeRec { uint64_t t; int idx, ntiles, qn, c; };
+constexpr int PROBE_SLOTS = 32, PROBE_BLOCKS = 256, PROBE_RECS = 640;
+__device__ ProbeRec g_attn_probe[PROBE_SLOTS][PROBE_BLOCKS][PROBE_RECS];
+__device__ __forceinline__ void probe_mark(const AttnArgs& a, int& k, int idx, int nt, int qn, int c) {
+  if (threadIdx.x == 0 && a.probe_slot < PROBE_SLOTS && blockIdx.x < PROBE_BLOCKS && k < PROBE_RECS) {
+    ProbeRec r;
+    r.t = __builtin_amdgcn_s_memrealtime();
+    r.idx = idx; r.ntiles = nt; r.qn = qn; r.c = c;
+    g_attn_probe[a.probe_slot][blockIdx.x][k] = r;
+  }
+  ++k;
+}
+#define PROBE(...) probe_mark(a, probe_k, __VA_ARGS__)
+#else
+#define PROBE(...) ((void)0)
+#endif
 
 constexpr int KT = 32;                  // keys per tile
 constexpr int PREFILL_ROWS = 128;       // (query, head) rows per work item: 32 per wave
@@ -51,6 +75,9 @@ constexpr int PREFILL_ROWS = 128;       // (query, head) rows per work item: 32 
 // 2^OVERFLOW_LOG2 (well inside fp32 and bf16 range) before an item is redone.
 constexpr float OVERFLOW_LOG2 = 64.0f;
 constexpr int BUFFER_CONFIG = 0x00020000;   // raw buffer resource, 32-bit data format
+// an offset past every range a store uses here (ranges stay below 2^31 bytes,
+// so adding the access size cannot wrap): such a store is dropped
+constexpr int OUT_OF_RANGE = (int)0x80000000u;
 
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
@@ -141,6 +168,10 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   using S = AttnTileShape<D>;
   constexpr int KS = D / 16;        // 16-dim steps of S^T
   constexpr int DT = D / 32;        // 32-dim tiles of O^T
+  // vector memory instructions of an item's epilogue: its rows (32 per wave,
+  // ROWS_PER_INST per store) and one LSE store
+  constexpr int EPI_STORES = 32 / S::ROWS_PER_INST + 1;
+  static_assert(EPI_STORES <= 63, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
   __shared__ int s_items[2];
 
@@ -356,6 +387,12 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     begin(rec);
   }
   int idx_n = -1;
+  bool begun_under_epilogue = false;   // PIPE: this item's first loads precede the last item's stores
+  int idx_after = -1;                  // PIPE: the item after the next one, claimed before those stores
+#ifdef SBSA_ATTN_PROBE
+  int probe_k = 0;
+#endif
+  PROBE(-2, 0, 0, 0);
   for (; idx >= 0; idx = idx_n) {
     // this item, as begin() left it
     const int h = __builtin_amdgcn_readfirstlane(b_h), c = __builtin_amdgcn_readfirstlane(b_c);
@@ -368,8 +405,13 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     const int qidx_r = b_qidx;
     const bool local = c < 0;
     const int ntiles = max(1, (nkeys + KT - 1) / KT);
-    idx_n = next_index();
-    if (idx_n >= 0) rec = a.items[idx_n];
+    PROBE(idx, ntiles, qn, c);
+    if (!begun_under_epilogue) {
+      idx_n = next_index();
+      if (idx_n >= 0) rec = a.items[idx_n];
+    } else {
+      idx_n = idx_after;      // claimed, and its record loaded, before the last epilogue's stores
+    }
     // once, after this item's first tiles are in (every wave has read its
     // slot by then); the next item's first step publishes it
     bool prefetched = false;
@@ -622,7 +664,13 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
       l_part = 0.f;
       lmax_all = NEG_INF;
-      __builtin_amdgcn_s_waitcnt(0);
+      if (PIPE && pass == 0 && begun_under_epilogue) {
+        // the first tiles were issued before the previous item's EPI_STORES
+        // stores: wait for every load but leave those stores in flight
+        __builtin_amdgcn_s_waitcnt((EPI_STORES & 15) | ((EPI_STORES >> 4) << 14) | (7 << 4));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0);
+      }
       __syncthreads();
       prefetch_queries();
       f32x16_t sA, sB;
@@ -658,8 +706,15 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       }
     }
 
-    // PIPE: the next item's Q and first tiles load under this item's epilogue
-    if (PIPE && idx_n >= 0) begin(rec);
+    // PIPE: the next item's Q and first tiles load under this item's epilogue,
+    // and the item after it is claimed and its record loaded before the
+    // epilogue's stores, so that no wait of the next item waits for them
+    begun_under_epilogue = PIPE && idx_n >= 0;
+    if (PIPE && idx_n >= 0) {
+      begin(rec);
+      idx_after = next_index();
+      if (idx_after >= 0) rec = a.items[idx_after];
+    }
 
     // epilogue: normalise, then write the partial (or the local window) and
     // its LSE.  The rows go through this wave's own 32-row slice of a staging
@@ -670,11 +725,37 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     {
       const float l = halves_sum(l_part);
       const float inv = (l > 0.f) ? 1.0f / l : 0.f;
-      if (qidx_r >= 0 && g == 0) {
+      // PIPE: every store of the epilogue is issued by every lane (EPI_STORES
+      // per wave), through buffer resources over the item's rows: a lane
+      // without a row stores at an offset past the range, where the store is
+      // dropped.  The next item's first wait counts on that number.  The
+      // compact form keeps plain stores under the rows' conditions: the
+      // resources would take it past 384 registers per lane, and the index
+      // build's kernels would no longer fit beside its blocks.
+      if (!PIPE) {
+        if (qidx_r >= 0 && g == 0) {
+          const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
+          float* ldst = local ? (a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + row_j : nullptr)
+                              : a.part_lse + (entry0 + row_i) * G + row_j;
+          if (ldst) *ldst = lse;
+        }
+      } else {
         const float lse = (l > 0.f) ? (m_ref + log2f(l)) * 0.69314718055994531f : NEG_INF;
-        float* ldst = local ? (a.local_lse ? a.local_lse + (int64_t)qidx_r * a.Hq + h * G + row_j : nullptr)
-                            : a.part_lse + (entry0 + row_i) * G + row_j;
-        if (ldst) *ldst = lse;
+        const float* lbase;
+        int64_t lbytes, loff;
+        if (local) {
+          lbase = a.local_lse ? a.local_lse : reinterpret_cast<const float*>(a.q);
+          lbytes = a.local_lse ? (int64_t)a.Qc * a.Hq * 4 : 0;
+          loff = ((int64_t)qidx_r * a.Hq + h * G + row_j) * 4;
+        } else {
+          lbase = a.part_lse + entry0 * G;
+          lbytes = (int64_t)qn * G * 4;
+          loff = (int64_t)(row_i * G + row_j) * 4;
+        }
+        const __amdgpu_buffer_rsrc_t lrsrc = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)uniform_ptr(reinterpret_cast<const bf16_t*>(lbase)), 0, (int)lbytes, BUFFER_CONFIG);
+        const int off = (qidx_r >= 0 && g == 0) ? (int)loff : OUT_OF_RANGE;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), lrsrc, off, 0, 0);
       }
       // 16-byte chunk c of row r sits at chunk c ^ (r % 32) of the row.  Lane
       // (l32, g) holds dims 32 dt + 8 q4 + 4 g .. +3; a swap between the lane
@@ -711,6 +792,12 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       // reads first, then the stores, so no store waits on a single read
       constexpr int NR = 32 / S::ROWS_PER_INST;
       const int c16 = lane % S::CH;
+      const bf16_t* obase = local ? a.local_o + (int64_t)qb * a.lo_sq + (int64_t)(h * G) * a.lo_sh
+                                  : a.part_o + entry0 * G * D;
+      const int64_t obytes = local ? ((int64_t)(qn - 1) * a.lo_sq + (int64_t)(G - 1) * a.lo_sh + D) * 2
+                                   : (int64_t)qn * G * D * 2;
+      __amdgpu_buffer_rsrc_t orsrc;
+      if (PIPE) orsrc = __builtin_amdgcn_make_buffer_rsrc((void*)uniform_ptr(obase), 0, (int)obytes, BUFFER_CONFIG);
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         u32x4_t rows[NR / 2];
@@ -725,10 +812,18 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
           const int m = half * (NR / 2) + mm;
           const int RR = wave * 32 + m * S::ROWS_PER_INST + lane / S::CH;
           const int i = RR / G, j = RR % G;
-          bf16_t* dst = local ? a.local_o + (int64_t)(qb + i) * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh
-                              : a.part_o + ((entry0 + i) * G + j) * D;
-          // read once, later, by the combine: kept out of the way of the K/V in L2
-          if (i < qn) __builtin_nontemporal_store(rows[mm], reinterpret_cast<u32x4_t*>(dst + 8 * c16));
+          // read once, later, by the combine: non-temporal, kept out of the way
+          // of the K/V in L2
+          if (PIPE) {
+            const int64_t roff = local ? ((int64_t)i * a.lo_sq + (int64_t)j * a.lo_sh) * 2
+                                       : (int64_t)(i * G + j) * D * 2;
+            __builtin_amdgcn_raw_buffer_store_b128(rows[mm], orsrc, i < qn ? (int)roff + 16 * c16 : OUT_OF_RANGE,
+                                                   0, 2);
+          } else {
+            bf16_t* dst = local ? a.local_o + (int64_t)(qb + i) * a.lo_sq + (int64_t)(h * G + j) * a.lo_sh
+                                : a.part_o + ((entry0 + i) * G + j) * D;
+            if (i < qn) __builtin_nontemporal_store(rows[mm], reinterpret_cast<u32x4_t*>(dst + 8 * c16));
+          }
         }
       }
     }
@@ -737,6 +832,7 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       begin(rec);
     }
   }
+  PROBE(-3, 0, 0, 0);
 }
 
 
@@ -947,6 +1043,13 @@ int combine_dispatch(int D, int G, const int32_t* qmask, const int32_t* nvis,
 
 extern "C" {
 
+#ifdef SBSA_ATTN_PROBE
+int sbsa_probe_read(void* host, size_t bytes) {
+  if (bytes > sizeof(g_attn_probe)) bytes = sizeof(g_attn_probe);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_attn_probe), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 3;
+}
+#endif
+
 int sbsa_prefill_item_rows(void) { return PREFILL_ROWS; }
 
 int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queries,
@@ -996,9 +1099,14 @@ int sbsa_prefill_attend(const void* q, int64_t q_sq, int64_t q_sh, int num_queri
   a.Hkv = num_kv_heads;
   a.C = num_clusters;
   a.Hq = num_q_heads;
+  a.Qc = num_queries;
   a.chunk_start = chunk_start;
   a.wstart = wstart;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+#ifdef SBSA_ATTN_PROBE
+  static int probe_next = 0;
+  a.probe_slot = probe_next++;
+#endif
   int rc = attn_dispatch(dim, num_q_heads / num_kv_heads, a, grid, stream);
   if (rc) return rc;
   SBSA_CHECK_LAUNCH();
