@@ -152,6 +152,7 @@ class PartialsGuard:
 
     def __init__(self):
         self._pending = []
+        self._next = 0
         self.reruns = 0
         self.cap_entries = 0
 
@@ -160,15 +161,29 @@ class PartialsGuard:
         flag.copy_(queue[QUEUE_OVERFLOW:QUEUE_OVERFLOW + 1], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
-        self._pending.append((ev, flag, rerun))
+        self._pending.append((self._next, ev, flag, rerun))
+        self._next += 1
 
-    def poll(self, wait: bool = False) -> None:
+    def mark(self) -> int:
+        """A mark: the chunks watched from now on are not below it."""
+        return self._next
+
+    def poll(self, wait: bool = False, wait_below: int | None = None) -> None:
+        """Settle chunks: with ``wait`` every one; with ``wait_below`` exactly those watched
+        before that mark (waiting for them), so that which chunks run again, and the room
+        the later ones get, does not depend on timing; otherwise those whose flags have
+        arrived."""
         keep = []
-        for ev, flag, rerun in self._pending:
-            if wait:
+        for seq, ev, flag, rerun in self._pending:
+            if wait_below is not None and not wait:
+                if seq >= wait_below:
+                    keep.append((seq, ev, flag, rerun))
+                    continue
+                ev.synchronize()
+            elif wait:
                 ev.synchronize()
             elif not ev.query():
-                keep.append((ev, flag, rerun))
+                keep.append((seq, ev, flag, rerun))
                 continue
             if int(flag[0]):
                 self.reruns += 1
@@ -240,11 +255,15 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
               out.stride(0), out.stride(1), None, qn, hq, hkv, d, c,
               _lib.ptr(queue[QUEUE_OVERFLOW:]) if capped else None, s)
     if capped:
+        # a run again reads the run starts as this chunk's plan saw them: a token-order
+        # session may lay the runs out again (into its other store) before the flag is read
+        indptr_seen = bucket_indptr.clone() if guard is not None else bucket_indptr
+
         def rerun():
             exact = int(plan.nnz_d.item())
             if guard is not None:
                 guard.cap_entries = max(guard.cap_entries, exact + exact // 4)
-            kv_outer_execute(q, packed_kv, plan, exact, bucket_indptr,
+            kv_outer_execute(q, packed_kv, plan, exact, indptr_seen,
                              sm_scale=sm_scale, local_kv=local_kv, chunk_start=chunk_start,
                              wstart=wstart, out=out, grid=grid, timing=timing)
         if guard is not None:

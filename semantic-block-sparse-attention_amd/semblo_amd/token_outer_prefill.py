@@ -232,6 +232,7 @@ class TokenOuterPrefillSession:
             pending = self._append_assign(kp, start, stop, store_timing)
             self.snapshot.sizes.copy_(self.index.bucket_sizes)
             self.snapshot.chunk_start = start
+            pending["guard_mark"] = self.guard.mark()
             self._attend(q, qp, kk, vv, start, stop, out, timing)
             self._append_commit(pending, kk, vv, store_timing)
         self.next_start = stop
@@ -342,8 +343,11 @@ class TokenOuterPrefillSession:
         s = _lib.stream(kk.device)
         ids, rows, counts = pending["ids"], pending["rows"], pending["counts"]
         pending["ready"].synchronize()
-        # capped chunks whose overflow flags have arrived (no wait)
-        self.guard.poll()
+        # Capped chunks of earlier slices: their attention preceded this slice's assignment
+        # on the stream, so their flags are in and nothing waits.  One that overflowed runs
+        # again here, before this slice's repack: it reads the store its plan saw, which a
+        # repack since then has left in the session's other buffer until this one.
+        self.guard.poll(wait_below=pending.get("guard_mark", 0))
         host = self._host
         flags_h = host[:hkv]
         if bool((flags_h & 2).any()):
@@ -362,9 +366,6 @@ class TokenOuterPrefillSession:
                 # always fits; the reference's intermediate layout is skipped.
                 reserve = reserved_layout(sizes_h + counts_h, start + n, self.tokens, width, align)
                 self.repacks_with_slice += 1
-            # a capped chunk run again reads the store as its plan saw it: settle every
-            # such chunk before the runs move
-            self.guard.finish()
             self._repack(start, reserve)
             rows, counts, _ = append_rows(ids, index.bucket_indptr, index.bucket_sizes, None)
         if kk.stride() != vv.stride() or kk.stride(-1) != 1:
