@@ -242,6 +242,11 @@ def test_build_with_empty_clusters_matches_the_oracle():
     want = ref.build_flat_index(product, codebook_seed=5, traces=traces, fit_steps=steps)
     empties = [sum(len(x[1]) for x in tr if x[0] == "empty") for tr in traces]
     assert empties[0] > 0 and empties[1] == 0 and empties[2] > 0, empties
+    # more empty iterations than the GPU restarts ahead (RESTARTS_AHEAD = 2): the
+    # iterations past those are restarted on the host and redone
+    from semblo_amd.state import RESTARTS_AHEAD
+    empty_iters = [sum(1 for x in tr if x[0] == "empty" and len(x[1]) > 0) for tr in traces]
+    assert empty_iters[0] > RESTARTS_AHEAD and empty_iters[2] > RESTARTS_AHEAD, empty_iters
     idx = _build_gpu(product, codebook_seed=5, fit_trace=trace)
     _check_index_invariants(idx, length)
     reps = _check_trace(product, idx, trace, want, steps, "restarts")
