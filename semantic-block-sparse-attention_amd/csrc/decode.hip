@@ -68,46 +68,67 @@ struct DecodeArgs {
   float inv_temp, beta, target, scale_log2;
 };
 
+#ifdef SBSA_DEC_PROBE
+// timing probe (a build flag, not in the product): wall clock per block and
+// phase of the last step, and per merge block its start and end
+__device__ uint64_t g_dec_probe[1024][16];
+__device__ uint64_t g_merge_probe[1024][2];
+#define DPROBE(k) do { if (threadIdx.x == 0) g_dec_probe[blockIdx.x * gridDim.y + blockIdx.y][(k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define DPROBEW(k) do { if ((threadIdx.x & 63) == 0) g_dec_probe[blockIdx.x * gridDim.y + blockIdx.y][(k) + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define DPROBE(k) ((void)0)
+#define DPROBEW(k) ((void)0)
+#endif
+
 constexpr int MAX_C = 1024;
 constexpr int MAX_SPLITS = 512;   // prompt + suffix splits of one step
 constexpr int DT = 32;            // keys per wave tile
-constexpr int ROW_CHUNK = 256;    // rows whose addresses a block resolves at once
 constexpr int MAX_TABLE = 256;    // suffix block-table entries staged in LDS
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
-// Per-wave LDS tile: DT rows of K then DT rows of V, each row D bf16 with
-// its 16-byte chunks permuted (K: chunk ^ (row % 8), V: chunk ^ 2 (row % 4))
-// so that the MFMA operand reads spread over the banks.
+// LDS layout of the step's attention: RC rows of V in tiles of 32 rows, each
+// row D bf16 with its 16-byte chunks permuted (chunk ^ 2 (row % 4)) so that the
+// transposing reads spread over the banks, then P^T [16][RC + 8] bf16.  K
+// rows go to registers: wave w holds NG groups of 16 keys.
 template <int D>
-struct DecodeTile {
+struct DecodeStep {
   static constexpr int ROW_BYTES = 2 * D;
   static constexpr int CH = D / 8;               // 16-byte chunks per row
   static constexpr int RPI = 64 / CH;            // rows per wave load instruction
-  static constexpr int INSTS = DT / RPI;         // load instructions per K (or V) tile
-  static constexpr int KV_BYTES = DT * ROW_BYTES;
-  static constexpr int WAVE_BYTES = 2 * KV_BYTES;
-  static constexpr size_t STAGE_BYTES = 4 * (size_t)WAVE_BYTES;
+  static constexpr int INSTS = DT / RPI;         // load instructions per V tile
+  static constexpr int TILE_BYTES = DT * ROW_BYTES;
+  static constexpr int RC = D >= 256 ? 192 : 384;  // rows per round
+  static constexpr int NG = RC / 64;             // 16-key groups per wave
+  static constexpr int DBW = D / 64;             // 16-dim blocks of O per wave
+  static constexpr size_t V_BYTES = (size_t)RC * ROW_BYTES;
+  static constexpr size_t LDS_BYTES = V_BYTES + (size_t)16 * (RC + 8) * 2;
 };
 
-// Dynamic LDS of the step kernel: the tile staging, or the selection's
-// routing vectors [16][D+8] bf16 and component weights [G][C] f32.
+// Dynamic LDS of the step kernel: the attention's V tiles and P^T, or the
+// selection's routing vectors [16][D+8] bf16 and component weights [G][C] f32.
 template <int D>
 size_t step_lds_bytes(int G, int C) {
   size_t sel = (size_t)16 * (D + 8) * 2 + (size_t)G * C * 4;
-  return sel > DecodeTile<D>::STAGE_BYTES ? sel : DecodeTile<D>::STAGE_BYTES;
+  return sel > DecodeStep<D>::LDS_BYTES ? sel : DecodeStep<D>::LDS_BYTES;
 }
 
 // ------------------------------------------------------------- selection ---
 // All 256 threads.  NK = clusters per lane of wave 0 (C <= 64 NK).  Leaves
 // the CSR of the head's selection in s_rstart / s_rcum (rcount entries) and
-// s_cnt = {rcount, rtokens}.
-template <int D, int NK, typename Prefetch>
-__device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, int pos_v, int64_t plen,
-                                             Prefetch prefetch, unsigned char* smem, int* s_rstart,
-                                             int* s_rcum, int* s_cnt) {
+// s_cnt = {rcount, rtokens}.  `prefetch` issues the caller's loads behind the
+// selection's first ones; `after_routing` runs in every wave once the routing
+// rows are in LDS (pos_v and plen are read only after it); `idle_loads` runs
+// in waves 1-3 while wave 0 bisects, and its copies into LDS have landed when
+// the selection returns.  Every load before the routing is issued in
+// straight-line code, so the routing waits for its own row only.
+template <int D, int NK, typename Prefetch, typename AfterRouting, typename IdleLoads>
+__device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, const int& pos_v,
+                                             const int64_t& plen, Prefetch prefetch,
+                                             AfterRouting after_routing, IdleLoads idle_loads,
+                                             unsigned char* smem, int* s_rstart, int* s_rcum, int* s_cnt) {
   constexpr int KS = D / 32;
   constexpr int LDQ = D + 8;
   bf16_t* svec = reinterpret_cast<bf16_t*>(smem);                   // [16][LDQ]
@@ -119,22 +140,25 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
   constexpr int PER = D / 64;
 
   // loads in the order of use: the router input row of this wave's first
-  // head (raw bits, converted at the routing), the codebook tiles, then the
-  // caller's.  Wave 0 copies the sizes and run starts straight into LDS
-  // (s_rcum / s_rstart, rewritten with the CSR later).
+  // head (raw bits, converted at the routing), the sizes and run starts, the
+  // codebook tiles, then the caller's.  No copy into LDS is in flight before
+  // the routing: the compiler waits for every load while one is.
   uint32_t vq[PER];
-  if (wave < G) {
-    const bf16_t* src = a.q_pre + (int64_t)(h * G + wave) * a.qp_sh;
+  DPROBE(12);
+  {
+    // every wave loads a valid row (waves past G: the last head's, unused)
+    const bf16_t* src = a.q_pre + (int64_t)(h * G + min(wave, G - 1)) * a.qp_sh;
 #pragma unroll
     for (int i = 0; i < PER; ++i) vq[i] = src[lane + 64 * i];
   }
-  if (wave == 0) {
-    for (int k = 0; k < nk; ++k) {
-      __builtin_amdgcn_global_load_lds((const void*)(a.sizes + h * C + 64 * k + lane),
-                                       (lds_void_t*)(s_rcum + 64 * k), 4, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(a.indptr + h * (C + 1) + 64 * k + lane),
-                                       (lds_void_t*)(s_rstart + 64 * k), 4, 0, 0);
-    }
+  // the clusters' sizes and run starts of this lane (read by wave 0 only; a
+  // cluster past C reads the last one's)
+  int sz[NK], ip[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const int c = min(64 * k + lane, C - 1);
+    sz[k] = a.sizes[h * C + c];
+    ip[k] = a.indptr[h * (C + 1) + c];
   }
   const bf16_t* cb = a.codebooks + (int64_t)h * 2 * C * half;
   auto load_cb = [&](int cbk, u32x4_t* b) {
@@ -147,9 +171,11 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     }
   };
   // the first two codebook tiles of this wave, in flight during the routing
+  // (loaded unconditionally, a tile past C clamped to the last, so that the
+  // routing's wait counts only the loads before its row)
   u32x4_t b0[KS], b1[KS];
-  if (wave < C / 16) load_cb(wave, b0);
-  if (wave + 4 < C / 16) load_cb(wave + 4, b1);
+  load_cb(min(wave, C / 16 - 1), b0);
+  load_cb(min(wave + 4, C / 16 - 1), b1);
   prefetch();
   // 1. routing vectors of the G query heads (rows >= G are zero)
   for (int e = threadIdx.x; e < 16 * (D / 8); e += 256) {
@@ -182,8 +208,11 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     }
 #pragma unroll
     for (int i = 0; i < PER; ++i) svec[t * LDQ + lane + 64 * i] = f2bf(v[i]);
+    DPROBE(13);
   }
   __syncthreads();
+  DPROBE(1);
+  after_routing();
   // 2. scores s[t][c] = v_t . c / tau on MFMA (16 rows, G real)
   u32x4_t aop[KS];
 #pragma unroll
@@ -208,6 +237,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     score_tile(cbk, b);
   }
   __syncthreads();
+  DPROBE(2);
   // 3. per component LSE, then w = exp(s - lse) in place
   for (int t = wave; t < G; t += 4) {
     float* row = ssc + t * C;
@@ -222,7 +252,9 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     for (int c = lane; c < C; c += 64) row[c] = __builtin_amdgcn_exp2f(__builtin_fmaf(row[c], LOG2E, -lse2));
   }
   __syncthreads();
+  DPROBE(3);
   if (wave != 0) {
+    idle_loads();
     // the token's K/V into the suffix store, once per head (a position past
     // the reservation is not written: the table does not cover it)
     const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
@@ -241,16 +273,12 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
       if (a.suffix_kpre && a.kpre_new)
         for (int d = threadIdx.x - 64; d < D; d += 192) a.suffix_kpre[at + d] = a.kpre_new[(int64_t)h * a.kn_sh + d];
     }
+    __builtin_amdgcn_s_waitcnt(0);       // the caller's copies into LDS (idle_loads) have landed
   } else {
     // 4. bisection and the CSR (wave 0); sizes are integers below 2^24, so
     //    the reference's fp32 sums are exact and equal these integer sums
-    __builtin_amdgcn_s_waitcnt(0);       // this wave's copies into LDS have landed
-    int sz[NK], ip[NK];
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      sz[k] = (k < nk) ? s_rcum[lane + 64 * k] : 0;
-      ip[k] = (k < nk) ? s_rstart[lane + 64 * k] : 0;
-    }
+    for (int k = 0; k < NK; ++k) sz[k] = (k < nk) ? sz[k] : 0;
     const float NEG = -3.4e38f, POS = 3.4e38f;
     float score[NK];
     int size[NK];
@@ -282,6 +310,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     live_total = wave_sum_i32_dpp(live_total);
     const float budget = (a.sink > 0) ? fmaxf(a.target - (float)a.sink, 0.f) : a.target;
     const bool all_fit = (float)live_total < budget;
+    DPROBE(14);
     // two bisection steps per round: the first step's mid and both possible
     // second mids are counted together (the same fp32 mids as one step at a time)
     for (int it = 0; it < a.iters; it += 2) {
@@ -310,6 +339,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
         }
       }
     }
+    DPROBE(15);
     const float theta = all_fit ? NEG : lo;
     int carry_n = 0, carry_tok = 0;
 #pragma unroll
@@ -346,23 +376,22 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     }
   }
   __syncthreads();
+  DPROBE(4);
 }
 
 // ------------------------------------------------------------------ step ---
 template <int D, int G, int NK>
 __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
-  using T = DecodeTile<D>;
+  using T = DecodeStep<D>;
   constexpr int KS = D / 32;
-  constexpr int DB = D / 16;
   static_assert(G <= 16, "query heads per KV head");
-  static_assert(16 * G * D <= (int)T::STAGE_BYTES, "wave partials fit the tile space");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_dec[];
   __shared__ int s_rcum[MAX_C];
   __shared__ int s_rstart[MAX_C];
   __shared__ int s_cnt[2];
   __shared__ int s_table[MAX_TABLE];
-  __shared__ const bf16_t* s_kaddr[ROW_CHUNK];
-  __shared__ const bf16_t* s_vaddr[ROW_CHUNK];
+  __shared__ const bf16_t* s_kaddr[T::RC];
+  __shared__ const bf16_t* s_vaddr[T::RC];
   __shared__ float s_m[4][16];
   __shared__ float s_l[4][16];
   const int h = blockIdx.x;
@@ -370,37 +399,49 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
   const int S = gridDim.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  // the position as a vector load (a scalar load would be waited on by the
-  // first LDS access)
-  const int pos_v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // the prompt length: tokens moved into the clusters after the prefill raise
-  // it on the device, so a captured step reads it there
-  const int64_t plen = a.plen_dev
-      ? (int64_t)__builtin_amdgcn_readfirstlane(
-            __hip_atomic_load(a.plen_dev, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      : a.prompt_len;
-  // suffix block table entries the live suffix may use (at most MAX_TABLE)
-  const int64_t tb0 = plen / a.BS;
-  const int64_t tb_n = a.max_tiles > 0 ? (plen + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
-  const bool table_in_lds = tb_n <= MAX_TABLE;
-  if (table_in_lds && wave == 0)   // copied straight into LDS; waited on in the selection
-    for (int k = 0; k * 64 < tb_n; ++k)
-      if (k * 64 + lane < tb_n)
-        __builtin_amdgcn_global_load_lds((const void*)(a.table + tb0 + k * 64 + lane),
-                                         (lds_void_t*)(s_table + 64 * k), 4, 0, 0);
-
+  DPROBE(0);
   // Q^T as the B operand: column l16 is query head h*G + l16 (zero past G);
   // in flight during the selection
   u32x4_t qr[KS];
-  auto load_q = [&]() {
+  // the position, and the prompt length on the device: tokens moved into the
+  // clusters after the prefill raise it, so a captured step reads it there.
+  // Both are vector loads issued behind the selection's first loads (a scalar
+  // load would be waited on by the first LDS access).
+  int pos_v = 0, plen_v = 0;
+  auto early_loads = [&]() {
+    pos_v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    plen_v = __hip_atomic_load(a.plen_dev ? a.plen_dev : a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool ok = l16 < G;
     const bf16_t* src = a.q_post + (int64_t)(h * G + (ok ? l16 : 0)) * a.q_sh + lg * 8;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qr[s] = ok ? *reinterpret_cast<const u32x4_t*>(src + s * 32) : u32x4_t{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 32);
+  };
+  // suffix block table entries the live suffix may use (at most MAX_TABLE),
+  // copied straight into LDS by wave 1 while wave 0 bisects
+  int64_t plen = a.prompt_len, tb0 = 0, tb_n = 0;
+  bool table_in_lds = false;
+  auto after_routing = [&]() {
+    if (a.plen_dev) plen = (int64_t)__builtin_amdgcn_readfirstlane(plen_v);
+    tb0 = plen / a.BS;
+    tb_n = a.max_tiles > 0 ? (plen + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
+    table_in_lds = tb_n <= MAX_TABLE;
+  };
+  auto table_loads = [&]() {
+    if (table_in_lds && wave == 1) {
+#pragma unroll
+      for (int k = 0; k < MAX_TABLE / 64; ++k)
+        if (k * 64 + lane < tb_n)
+          __builtin_amdgcn_global_load_lds((const void*)(a.table + tb0 + k * 64 + lane),
+                                           (lds_void_t*)(s_table + 64 * k), 4, 0, 0);
+    }
   };
 
-  select_phase<D, NK>(a, h, split == 0, pos_v, plen, load_q, smem_dec, s_rstart, s_rcum, s_cnt);
+  select_phase<D, NK>(a, h, split == 0, pos_v, plen, early_loads, after_routing, table_loads, smem_dec,
+                      s_rstart, s_rcum, s_cnt);
+  if (l16 >= G) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = u32x4_t{0, 0, 0, 0};
+  }
   const int64_t q_pos = __builtin_amdgcn_readfirstlane(pos_v);
 
   // this split's range of the head's key list (prompt rows, then suffix rows)
@@ -415,32 +456,37 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
   const int64_t pplane = a.packed_len * a.Hkv * D;
   const int64_t splane = a.suffix_nblk * a.BS * a.Hkv * D;
 
-  // fixed per-lane LDS offsets
+  // Rows are taken RC at a time (one round at the headline shape).  Wave w
+  // holds the K rows of 16-key groups w, w + 4, ... in registers, straight
+  // from memory, and computes S^T = K Q^T for them; every wave copies a share
+  // of the V rows into LDS.  P (bf16) goes through LDS, and each wave then
+  // accumulates O^T = V^T P^T for its own D/4 dims over all the round's keys,
+  // so the split's partial needs no fold across waves.
+  constexpr int RC = T::RC, NG = T::NG, DBW = T::DBW;
+  unsigned char* sV = smem_dec;                                        // RC/32 tiles of 32 V rows
+  bf16_t* sP = reinterpret_cast<bf16_t*>(smem_dec + T::V_BYTES);       // [16][RC + 8]
+  constexpr int LDP = RC + 8;
   const int cpos = lane % T::CH;
-  const int xb = (l16 >> 2) & 1, xl = l16 & 3;
-  const int kbase_even = l16 * T::ROW_BYTES + 64 * xb + 16 * (lg ^ xl);
-  const int kbase_odd = l16 * T::ROW_BYTES - 64 * xb + 16 * (lg ^ xl);
   const int z = (l16 >> 2) & 3;
   int vbase[4];
 #pragma unroll
   for (int dl = 0; dl < 4; ++dl)
     vbase[dl] = (lg * 4 + (l16 >> 2)) * T::ROW_BYTES + 32 * (dl ^ z) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
-  unsigned char* sK = smem_dec + wave * T::WAVE_BYTES;
-  unsigned char* sV = sK + T::KV_BYTES;
 
-  float m_run = -INFINITY, l_run = 0.f;          // of query head l16
-  f32x4_t o[DB];
+  float m_run = -INFINITY;       // of query head l16, log2 units, the same in every wave
+  float l_part = 0.f;            // this lane's share of the normaliser (its keys)
+  f32x4_t o[DBW];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) o[db] = f32x4_t{0, 0, 0, 0};
+  for (int j = 0; j < DBW; ++j) o[j] = f32x4_t{0, 0, 0, 0};
 
-  for (int c0 = r_lo; c0 < r_hi; c0 += ROW_CHUNK) {
-    const int cn = min(ROW_CHUNK, r_hi - c0);
-    {
-      // address of row c0 + tid of the key list (rows past cn: a valid dummy row)
-      const int oo = c0 + (int)threadIdx.x;
+  for (int c0 = r_lo; c0 < r_hi; c0 += RC) {
+    const int cn = min(RC, r_hi - c0);
+    for (int t = threadIdx.x; t < RC; t += 256) {
+      // address of row c0 + t of the key list (rows past cn: a valid dummy row)
+      const int oo = c0 + t;
       const bf16_t* kp = a.packed + (int64_t)h * D;
       const bf16_t* vp = kp + pplane;
-      if ((int)threadIdx.x < cn) {
+      if (t < cn) {
         if (oo < count) {
           int lo = 0, hi = rcount;
           while (lo < hi) {
@@ -466,115 +512,132 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
           }
         }
       }
-      s_kaddr[threadIdx.x] = kp;
-      s_vaddr[threadIdx.x] = vp;
+      s_kaddr[t] = kp;
+      s_vaddr[t] = vp;
     }
     __syncthreads();
-    for (int t0 = wave * DT; t0 < cn; t0 += 4 * DT) {
-      // gather the tile's K and V rows into this wave's LDS tile
+    DPROBE(5);
+    // this wave's K groups into registers: lane (l16, lg) holds key g*16 + l16,
+    // dims s*32 + lg*8 .. +7, the A operand of S^T
+    u32x4_t kr[NG][KS];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const int g = wave + 4 * j;
+      if (g * 16 < cn) {
+        const bf16_t* row = s_kaddr[g * 16 + l16] + lg * 8;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kr[j][s] = *reinterpret_cast<const u32x4_t*>(row + s * 32);
+      }
+    }
+    // V tiles w, w + 4, ... into LDS (16-byte chunks permuted by chunk ^ 2 (row % 4))
+    for (int t0 = wave * 32; t0 < cn; t0 += 128) {
+      unsigned char* dst = sV + (t0 / 32) * T::TILE_BYTES;
 #pragma unroll
       for (int m = 0; m < T::INSTS; ++m) {
         const int r = m * T::RPI + lane / T::CH;
-        const bf16_t* kr = s_kaddr[t0 + r];
         const bf16_t* vr = s_vaddr[t0 + r];
-        __builtin_amdgcn_global_load_lds((const void*)(kr + 8 * (cpos ^ (r & 7))),
-                                         (lds_void_t*)(sK + m * 1024), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const void*)(vr + 8 * (cpos ^ ((r & 3) << 1))),
-                                         (lds_void_t*)(sV + m * 1024), 16, 0, 0);
+                                         (lds_void_t*)(dst + m * 1024), 16, 0, 0);
       }
-      __builtin_amdgcn_s_waitcnt(0);
-      // S^T = K Q^T: lane holds keys kb*16 + lg*4 + i of query head l16
-      f32x4_t sacc[2] = {f32x4_t{0, 0, 0, 0}, f32x4_t{0, 0, 0, 0}};
+    }
+    // S^T: lane holds keys g*16 + lg*4 + i of query head l16
+    f32x4_t sc[NG];
+    float mx = -INFINITY;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const unsigned char* kb0 = sK + ((s & 1) ? kbase_odd : kbase_even) + 64 * s;
+    for (int j = 0; j < NG; ++j) {
+      const int g = wave + 4 * j;
+      sc[j] = f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      if (g * 16 < cn) {
+        f32x4_t acc = f32x4_t{0, 0, 0, 0};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          u32x4_t ka = *reinterpret_cast<const u32x4_t*>(kb0 + kb * 16 * T::ROW_BYTES);
-          sacc[kb] = mfma16x16x32(as_bf16x8(ka), as_bf16x8(qr[s]), sacc[kb]);
-        }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int s = 0; s < KS; ++s) acc = mfma16x16x32(as_bf16x8(kr[j][s]), as_bf16x8(qr[s]), acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (t0 + kb * 16 + lg * 4 + i >= cn) sacc[kb][i] = -INFINITY;
-          mx = fmaxf(mx, sacc[kb][i]);
+          const float v = (g * 16 + lg * 4 + i < cn) ? acc[i] * a.scale_log2 : -INFINITY;
+          sc[j][i] = v;
+          mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      mx *= a.scale_log2;
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      float sum = 0.f;
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (lg == 0) s_m[wave][l16] = mx;
+    __syncthreads();
+    const float m_new = fmaxf(m_run, fmaxf(fmaxf(s_m[0][l16], s_m[1][l16]), fmaxf(s_m[2][l16], s_m[3][l16])));
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    float sum = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int j = 0; j < NG; ++j) {
+      const int g = wave + 4 * j;
+      if (g * 16 < RC) {
+        float pv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][i], a.scale_log2, -m_use));
-          sacc[kb][i] = p;
-          sum += p;
+          pv[i] = __builtin_amdgcn_exp2f(sc[j][i] - m_use);
+          sum += pv[i];
         }
-      sum += __shfl_xor(sum, 16, 64);
-      sum += __shfl_xor(sum, 32, 64);
-      l_run = l_run * alpha + sum;
-      m_run = m_new;
-      // P^T as the B operand: keys {4 lg..4 lg+3, 16+4 lg..16+4 lg+3} of head l16
+        u32x2_t pk;
+        pk.x = pack2bf(pv[0], pv[1]);
+        pk.y = pack2bf(pv[2], pv[3]);
+        *reinterpret_cast<u32x2_t*>(&sP[l16 * LDP + g * 16 + lg * 4]) = pk;
+      }
+    }
+    l_part = l_part * alpha + sum;
+#pragma unroll
+    for (int j = 0; j < DBW; ++j) o[j] = o[j] * alpha;
+    __builtin_amdgcn_s_waitcnt(0);           // this wave's V copies have landed
+    __syncthreads();
+    // O^T += V^T P^T over the round's keys, 32 at a time, for dims
+    // (wave * DBW + j) * 16 .. +15; P^T as the B operand: keys
+    // {4 lg..4 lg+3, 16+4 lg..16+4 lg+3} of head l16 (V^T is read in that order)
+    for (int t0 = 0; t0 < cn; t0 += 32) {
+      const unsigned char* tile = sV + (t0 / 32) * T::TILE_BYTES;
       u32x4_t pb;
-      pb.x = pack2bf(sacc[0][0], sacc[0][1]);
-      pb.y = pack2bf(sacc[0][2], sacc[0][3]);
-      pb.z = pack2bf(sacc[1][0], sacc[1][1]);
-      pb.w = pack2bf(sacc[1][2], sacc[1][3]);
-      // O^T = alpha O^T + V^T P^T (V^T by transposing LDS reads in the same key order)
+      const u32x2_t p0 = *reinterpret_cast<const u32x2_t*>(&sP[l16 * LDP + t0 + lg * 4]);
+      const u32x2_t p1 = *reinterpret_cast<const u32x2_t*>(&sP[l16 * LDP + t0 + 16 + lg * 4]);
+      pb.x = p0.x; pb.y = p0.y; pb.z = p1.x; pb.w = p1.y;
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
+      for (int j = 0; j < DBW; ++j) {
+        const int db = wave * DBW + j;
         s16x4_t part[2];
 #pragma unroll
         for (int hlf = 0; hlf < 2; ++hlf) {
-          const unsigned char* p = sV + vbase[db & 3] + hlf * 16 * T::ROW_BYTES + 128 * (db >> 2);
+          const unsigned char* p = tile + vbase[db & 3] + hlf * 16 * T::ROW_BYTES + 128 * (db >> 2);
           part[hlf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
         }
         u32x4_t va;
         __builtin_memcpy(&va, part, 16);
-        o[db] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb), o[db] * alpha);
+        o[j] = mfma16x16x32(as_bf16x8(va), as_bf16x8(pb), o[j]);
       }
     }
-    __syncthreads();
+    if (c0 + RC < r_hi) __syncthreads();     // the next round reuses the V tiles, P and addresses
   }
+  DPROBEW(8);
 
-  // fold the four waves into the split's partial (tile space reused)
-  float* s_acc = reinterpret_cast<float*>(smem_dec);   // [4][G][D]
+  // the split's partial: this wave's dims of O (relative to m_run), and the
+  // normaliser summed over the lanes' and the waves' keys
+  float lsum = l_part;
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (lg == 0) s_l[wave][l16] = lsum;
   if (l16 < G) {
-    if (lg == 0) {
-      s_m[wave][l16] = m_run;
-      s_l[wave][l16] = l_run;
-    }
+    const int hq = h * G + l16;
+    float* dst = a.pacc + ((int64_t)hq * S + split) * D + lg * 4;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s_acc[(wave * G + l16) * D + db * 16 + lg * 4 + i] = o[db][i];
+    for (int j = 0; j < DBW; ++j)
+      *reinterpret_cast<f32x4_t*>(dst + (wave * DBW + j) * 16) = o[j];
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int j = e / D, d = e % D;
-    const float mx = fmaxf(fmaxf(s_m[0][j], s_m[1][j]), fmaxf(s_m[2][j], s_m[3][j]));
-    const float mu = (mx == -INFINITY) ? 0.f : mx;
-    float num = 0.f, den = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float sc = (s_m[w][j] == -INFINITY) ? 0.f : exp2f(s_m[w][j] - mu);
-      num += s_acc[(w * G + j) * D + d] * sc;
-      den += s_l[w][j] * sc;
-    }
+  DPROBE(6);
+  if (threadIdx.x < G) {
+    const int j = threadIdx.x;
     const int hq = h * G + j;
-    a.pacc[((int64_t)hq * S + split) * D + d] = num;
-    if (d == 0) {
-      a.pm[(int64_t)hq * S + split] = mx;
-      a.pl[(int64_t)hq * S + split] = den;
-    }
+    a.pm[(int64_t)hq * S + split] = m_run;   // every lane of head j holds the same m_run
+    a.pl[(int64_t)hq * S + split] = (s_l[0][j] + s_l[1][j]) + (s_l[2][j] + s_l[3][j]);
   }
+  DPROBE(7);
 }
 
 // ----------------------------------------------------------------- merge ---
@@ -588,6 +651,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) 
   __shared__ float s_red[4][64];
   const int hq = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#ifdef SBSA_DEC_PROBE
+  if (threadIdx.x == 0) g_merge_probe[blockIdx.x * gridDim.y + blockIdx.y][0] = __builtin_amdgcn_s_memrealtime();
+#endif
   const int d = blockIdx.y * 64 + lane;
   const float* src = a.pacc + (int64_t)hq * S * D + d;
   float v[PRE];
@@ -636,6 +702,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) 
     if (lane == 0 && blockIdx.y == 0 && a.out_lse)
       a.out_lse[hq] = (den > 0.f) ? (mu + log2f(den)) * 0.69314718055994531f : -INFINITY;
   }
+#ifdef SBSA_DEC_PROBE
+  if (threadIdx.x == 0) g_merge_probe[blockIdx.x * gridDim.y + blockIdx.y][1] = __builtin_amdgcn_s_memrealtime();
+#endif
 }
 
 template <int D, int G, int NK>
@@ -860,3 +929,11 @@ int sbsa_decode_step_noalloc(const void* q_post, int64_t q_sh, const void* q_pre
 }
 
 }  // extern "C"
+
+#ifdef SBSA_DEC_PROBE
+extern "C" int sbsa_dec_probe_read(void* host, size_t bytes, void* host_merge, size_t merge_bytes) {
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dec_probe), bytes) != hipSuccess) return 1;
+  if (hipMemcpyFromSymbol(host_merge, HIP_SYMBOL(g_merge_probe), merge_bytes) != hipSuccess) return 1;
+  return 0;
+}
+#endif
