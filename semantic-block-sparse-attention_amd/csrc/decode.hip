@@ -86,6 +86,7 @@ constexpr int DT = 32;            // keys per wave tile
 constexpr int MAX_TABLE = 256;    // suffix block-table entries staged in LDS
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const u32x4_t global_u32x4_t;
 typedef __attribute__((ext_vector_type(4))) short s16x4_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
@@ -416,14 +417,18 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4_t*>(src + s * 32);
   };
-  // suffix block table entries the live suffix may use (at most MAX_TABLE),
+  // suffix block table entries the live suffix uses (at most MAX_TABLE),
   // copied straight into LDS by wave 1 while wave 0 bisects
   int64_t plen = a.prompt_len, tb0 = 0, tb_n = 0;
   bool table_in_lds = false;
   auto after_routing = [&]() {
     if (a.plen_dev) plen = (int64_t)__builtin_amdgcn_readfirstlane(plen_v);
+    // the blocks of the live suffix, positions plen .. plen + nsuf - 1
+    const int64_t qp = __builtin_amdgcn_readfirstlane(pos_v);
+    int64_t nsuf = qp - plen + 1;
+    nsuf = nsuf < 0 ? 0 : (nsuf > (int64_t)a.max_tiles * 16 ? (int64_t)a.max_tiles * 16 : nsuf);
     tb0 = plen / a.BS;
-    tb_n = a.max_tiles > 0 ? (plen + (int64_t)a.max_tiles * 16 - 1) / a.BS - tb0 + 1 : 0;
+    tb_n = nsuf > 0 ? (plen + nsuf - 1) / a.BS - tb0 + 1 : 0;
     table_in_lds = tb_n <= MAX_TABLE;
   };
   auto table_loads = [&]() {
@@ -504,7 +509,8 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
             kp = a.k_new + (int64_t)h * a.kn_sh;
             vp = a.v_new + (int64_t)h * a.kn_sh;
           } else {
-            const int64_t blk = p / a.BS;
+            // p <= the query position (an int32), the block size is positive
+            const int64_t blk = (int64_t)((uint32_t)p / (uint32_t)a.BS);
             const int64_t off = p - blk * a.BS;
             const int64_t phys = table_in_lds ? (int64_t)s_table[blk - tb0] : (int64_t)a.table[blk];
             kp = a.suffix_kv + ((phys * a.BS + off) * a.Hkv + h) * D;
@@ -524,9 +530,11 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
     for (int j = 0; j < NG; ++j) {
       const int g = wave + 4 * j;
       if (g * 16 < cn) {
-        const bf16_t* row = s_kaddr[g * 16 + l16] + lg * 8;
+        // global (not flat) loads: a flat load is also counted by the LDS
+        // counter, which the V copies below wait on for their addresses
+        const global_u32x4_t* row = (const global_u32x4_t*)(s_kaddr[g * 16 + l16] + lg * 8);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) kr[j][s] = *reinterpret_cast<const u32x4_t*>(row + s * 32);
+        for (int s = 0; s < KS; ++s) kr[j][s] = row[s * 4];
       }
     }
     // V tiles w, w + 4, ... into LDS (16-byte chunks permuted by chunk ^ 2 (row % 4))
@@ -772,6 +780,7 @@ int decode_step_impl(const void* q_post, int64_t q_sh, const void* q_pre, int64_
   if (num_kv_heads < 1 || num_q_heads % num_kv_heads || num_splits < 1 || suffix_splits < 1)
     return SBSA_ERR_ARG;
   if (q_sh % 8 || qp_sh % 8 || kn_sh % 8 || max_tiles < 0) return SBSA_ERR_ARG;
+  if (suffix_block < 1 || suffix_nblk < 1) return SBSA_ERR_ARG;
   const int G = num_q_heads / num_kv_heads;
   const int C = num_clusters;
   if (C % 64 || C > MAX_C) return SBSA_ERR_UNSUPPORTED;
