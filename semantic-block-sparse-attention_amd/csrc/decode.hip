@@ -125,7 +125,7 @@ size_t step_lds_bytes(int G, int C) {
 // in waves 1-3 while wave 0 bisects, and its copies into LDS have landed when
 // the selection returns.  Every load before the routing is issued in
 // straight-line code, so the routing waits for its own row only.
-template <int D, int NK, typename Prefetch, typename AfterRouting, typename IdleLoads>
+template <int D, int G, int NK, typename Prefetch, typename AfterRouting, typename IdleLoads>
 __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool leader, const int& pos_v,
                                              const int64_t& plen, Prefetch prefetch,
                                              AfterRouting after_routing, IdleLoads idle_loads,
@@ -135,7 +135,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
   bf16_t* svec = reinterpret_cast<bf16_t*>(smem);                   // [16][LDQ]
   float* ssc = reinterpret_cast<float*>(smem + 16 * LDQ * 2);        // [G][C]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int C = a.C, G = a.G;
+  const int C = a.C;
   const int half = D / 2;
   const int nk = C / 64;
   constexpr int PER = D / 64;
@@ -239,21 +239,6 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
   }
   __syncthreads();
   DPROBE(2);
-  // 3. per component LSE, then w = exp(s - lse) in place
-  for (int t = wave; t < G; t += 4) {
-    float* row = ssc + t * C;
-    float m = -INFINITY;
-    for (int c = lane; c < C; c += 64) m = fmaxf(m, row[c]);
-    m = wave_max_dpp(m);
-    float l = 0.f;
-    constexpr float LOG2E = 1.4426950408889634f;
-    for (int c = lane; c < C; c += 64) l += __builtin_amdgcn_exp2f((row[c] - m) * LOG2E);
-    l = wave_sum_dpp(l);
-    const float lse2 = m * LOG2E + __builtin_amdgcn_logf(l);    // log2 of the normaliser
-    for (int c = lane; c < C; c += 64) row[c] = __builtin_amdgcn_exp2f(__builtin_fmaf(row[c], LOG2E, -lse2));
-  }
-  __syncthreads();
-  DPROBE(3);
   if (wave != 0) {
     idle_loads();
     // the token's K/V into the suffix store, once per head (a position past
@@ -276,10 +261,44 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     }
     __builtin_amdgcn_s_waitcnt(0);       // the caller's copies into LDS (idle_loads) have landed
   } else {
-    // 4. bisection and the CSR (wave 0); sizes are integers below 2^24, so
+    // 4. bisection and the CSR; sizes are integers below 2^24, so
     //    the reference's fp32 sums are exact and equal these integer sums
 #pragma unroll
     for (int k = 0; k < NK; ++k) sz[k] = (k < nk) ? sz[k] : 0;
+    // 3. per component LSE over the clusters, then each cluster's weight
+    //    p_c = sum_t exp(s_tc - lse_t): the same sums in the same order as a
+    //    pass per component, with the G components' reductions interleaved
+    constexpr float LOG2E = 1.4426950408889634f;
+    float sv[G][NK], mt[G], lt[G];
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      mt[t] = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        sv[t][k] = (k < nk) ? ssc[t * C + lane + 64 * k] : 0.f;
+        if (k < nk) mt[t] = fmaxf(mt[t], sv[t][k]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < G; ++t) mt[t] = wave_max_dpp(mt[t]);
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      lt[t] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NK; ++k)
+        if (k < nk) lt[t] += __builtin_amdgcn_exp2f((sv[t][k] - mt[t]) * LOG2E);
+    }
+#pragma unroll
+    for (int t = 0; t < G; ++t) lt[t] = wave_sum_dpp(lt[t]);
+    float pw[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) pw[k] = 0.f;
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      const float lse2 = mt[t] * LOG2E + __builtin_amdgcn_logf(lt[t]);    // log2 of the normaliser
+#pragma unroll
+      for (int k = 0; k < NK; ++k) pw[k] += __builtin_amdgcn_exp2f(__builtin_fmaf(sv[t][k], LOG2E, -lse2));
+    }
     const float NEG = -3.4e38f, POS = 3.4e38f;
     float score[NK];
     int size[NK];
@@ -291,8 +310,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
       size[k] = 0;
       if (k < nk) {
         const int c = lane + 64 * k;
-        float p = 0.f;
-        for (int t = 0; t < G; ++t) p += ssc[t * C + c];
+        const float p = pw[k];
         const int s = (a.sink > 0 && c == 0) ? 0 : sz[k];
         size[k] = s;
         const bool live = s > 0;
@@ -441,7 +459,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
     }
   };
 
-  select_phase<D, NK>(a, h, split == 0, pos_v, plen, early_loads, after_routing, table_loads, smem_dec,
+  select_phase<D, G, NK>(a, h, split == 0, pos_v, plen, early_loads, after_routing, table_loads, smem_dec,
                       s_rstart, s_rcum, s_cnt);
   if (l16 >= G) {
 #pragma unroll
