@@ -189,12 +189,13 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
       b[s] = *reinterpret_cast<const u32x4_t*>(cb + ((int64_t)part * C + cc) * half + (d - part * half));
     }
   };
-  // the first two codebook tiles of this wave, in flight during the routing
-  // (loaded unconditionally, a tile past C clamped to the last, so that the
-  // routing's wait counts only the loads before its row)
-  u32x4_t b0[KS], b1[KS];
-  load_cb(min(wave, C / 16 - 1), b0);
-  load_cb(min(wave + 4, C / 16 - 1), b1);
+  // this wave's first PT codebook tiles (all of them up to C = 256), in flight
+  // during the routing (loaded unconditionally, a tile past C clamped to the
+  // last, so that the routing's wait counts only the loads before its row)
+  constexpr int PT = NK < 2 ? 2 : (NK > 4 ? 4 : NK);
+  u32x4_t bt[PT][KS];
+#pragma unroll
+  for (int i = 0; i < PT; ++i) load_cb(min(wave + 4 * i, C / 16 - 1), bt[i]);
   prefetch();
   // 1. routing vectors of the G query heads (rows >= G are zero)
   for (int e = threadIdx.x; e < 16 * (D / 8); e += 256) {
@@ -248,9 +249,10 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
       if (t < G) ssc[t * C + cc] = acc[i] * a.inv_temp;
     }
   };
-  if (wave < C / 16) score_tile(wave, b0);
-  if (wave + 4 < C / 16) score_tile(wave + 4, b1);
-  for (int cbk = wave + 8; cbk < C / 16; cbk += 4) {
+#pragma unroll
+  for (int i = 0; i < PT; ++i)
+    if (wave + 4 * i < C / 16) score_tile(wave + 4 * i, bt[i]);
+  for (int cbk = wave + 4 * PT; cbk < C / 16; cbk += 4) {
     u32x4_t b[KS];
     load_cb(cbk, b);
     score_tile(cbk, b);
