@@ -248,7 +248,7 @@ int sbsa_prefill_combine(const int32_t* qmask, const int32_t* nvis, const int32_
  * suffix_kpre (optional, [Hkv, dim] at kn_sh / [suffix_nblk, suffix_block,
  * Hkv, dim]): the token's pre-RoPE key is stored beside its K/V, for the
  * flush's routing (arena.py:138-141).  num_splits + suffix_splits
- * <= 512.  No host reads, no allocation: capturable in a HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
+ * <= 512; suffix_block and suffix_nblk at least 1 (else SBSA_ERR_ARG).  No host reads, no allocation: capturable in a HIP graph.  csr_out (optional) receives [rstart, rlen, rcum] ([3, Hkv, C])
  * then rcount [Hkv] and rtokens [Hkv]; of each head's C entries only the first
  * rcount[h] are written by the step (the rest keep earlier contents). */
 size_t sbsa_decode_workspace_bytes(int num_q_heads, int num_kv_heads, int num_clusters, int dim,
