@@ -75,13 +75,15 @@ def dense_chunk(length: int, hq: int, hkv: int, d: int, cs: int, ce: int, seed: 
 
 
 def decode_steps(length: int, hq: int, hkv: int, d: int, seed: int, steps: int = 4,
-                 splits: int = 8) -> None:
+                 splits: int = 8, target: int = 0) -> None:
     """Decode steps over the prompt's selection and the suffix store
-    (fused_decode.py:393-521) against fp64 over the step's own selection."""
+    (fused_decode.py:393-521) against fp64 over the step's own selection.  A
+    large ``target`` with few ``splits`` gives each split several rounds of rows."""
     from semblo_amd.arena import DecodeArena
     from semblo_amd.fused_decode import fused_decode_step
     from semblo_amd.synthetic import decode_queries, mixture_layer
-    length, hq, hkv, d, seed, steps, splits = map(int, (length, hq, hkv, d, seed, steps, splits))
+    length, hq, hkv, d, seed, steps, splits, target = map(int, (length, hq, hkv, d, seed, steps, splits, target))
+    target = target or length // 16
     inp = mixture_layer(length, hq, hkv, d, mixtures=16, seg=(32, 256), seed=seed)
     idx = _index(inp.k, length, seed)
     idx.pack_prompt_kv(inp.k, inp.v)
@@ -101,7 +103,7 @@ def decode_steps(length: int, hq: int, hkv: int, d: int, seed: int, steps: int =
         pos = torch.tensor([length + t], dtype=torch.int32)
         fused_decode_step(_Layer(), arena, q_post=qs[t:t + 1], q_pre=qs[t:t + 1], positions=pos,
                           k_post=kn[t:t + 1], v_states=vn[t:t + 1], output=out, temperature=0.1,
-                          beta=0.25, target_tokens=length // 16, sm_scale=d ** -0.5,
+                          beta=0.25, target_tokens=target, sm_scale=d ** -0.5,
                           num_splits=splits, iters=16, csr_out=csr)
         sel = torch.zeros(hkv, c, dtype=torch.bool)
         rstart = csr[:n].view(hkv, c)

@@ -62,6 +62,12 @@ def test_emulated_decode_steps():
     _run("decode_steps", 1024, 8, 2, 128, 5)
 
 
+def test_emulated_decode_steps_in_several_rounds():
+    # D = 256, G = 4 (192-row rounds), one prompt split and one suffix split and
+    # a 512-token budget: each split takes its rows in two rounds
+    _run("decode_steps", 1024, 4, 1, 256, 7, 1, 1, 512)
+
+
 def test_gpu_selection_and_append_tests_under_emulation():
     """The selection tests and the token-order append tests, run unchanged on the
     emulated kernels (each kernel's every memory access under the sanitizer)."""
