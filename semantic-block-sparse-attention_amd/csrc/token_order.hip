@@ -174,7 +174,9 @@ __global__ __launch_bounds__(256) void nearest_cluster_kernel(
 // ---------------------------------------------------------------- append rows --
 // One block (16 waves) per KV head.  Wave w takes a contiguous segment of the
 // slice's positions; the ids of 64 positions at a time are grouped by value
-// with ballots, so a key's rank among the earlier keys of its cluster is
+// with ballots (on the scalar unit, one round per distinct id; the running
+// counts are then read once per lane and raised once per id), so a key's rank
+// among the earlier keys of its cluster is
 //   (keys of that cluster in earlier segments) + (earlier in this segment)
 //   + (earlier lanes of this group).
 // Pass 1 counts per segment, a scan over the segments gives each cluster's
@@ -223,24 +225,34 @@ __global__ __launch_bounds__(1024) void append_rows_kernel(
           if (pass == 1) rows[(int64_t)h * n + p] = -1;
           else atomicOr(&s_flag, 2);
         }
+        // the lane's rank among the earlier lanes with its id, and (in the first
+        // lane of each id) the id's count in the group: one round per distinct id,
+        // on the scalar unit and the lane masks only
         bool pending = id >= 0;
+        int rank = 0, lead_count = 0;
         for (;;) {
           const uint64_t act = __ballot(pending);
           if (!act) break;
           const int lead = __ffsll((unsigned long long)act) - 1;
-          const int lid = __shfl(id, lead, 64);
+          const int lid = __builtin_amdgcn_readlane(id, lead);
           const bool hit = pending && id == lid;
           const uint64_t m = __ballot(hit);
-          const int start = pass ? base[lid] + mine[lid] : 0;
           if (hit) {
-            if (pass) rows[(int64_t)h * n + p] = start + __popcll(m & below);
+            rank = __popcll(m & below);
             pending = false;
           }
-          // every lane has read mine[lid] before the lead lane adds to it (in
-          // order on the GPU; the barrier keeps the compiler from moving them)
-          __builtin_amdgcn_wave_barrier();
-          if (lane == lead) mine[lid] += __popcll(m);
+          if (lane == lead) lead_count = __popcll(m);
         }
+        // the group's keys follow the segment's earlier keys of their cluster:
+        // read the running counts, then add the group's (one lane per id)
+        if (id >= 0) {
+          if (pass == 1) rows[(int64_t)h * n + p] = base[id] + mine[id] + rank;
+        }
+        // every lane has read mine[] before the first lanes add to it (in order on
+        // the GPU; the barrier keeps the compiler from moving them)
+        __builtin_amdgcn_wave_barrier();
+        if (lead_count > 0) mine[id] += lead_count;
+        __builtin_amdgcn_wave_barrier();
       }
     }
     __syncthreads();
