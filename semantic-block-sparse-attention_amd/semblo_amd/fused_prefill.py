@@ -69,9 +69,7 @@ class ChunkPlan:
                             qmask=self.kv.qmask, theta=self.theta))
 
     def tensors(self):
-        kv = self.kv
-        return (self.causal_sizes, self.tokens, kv.qmask, kv.nvis, kv.qvals, kv.counts,
-                kv.rev_indptr, kv.nnz_d, kv.qrank)
+        return (self.causal_sizes, self.tokens, *self.kv.tensors())
 
 
 def chunk_window_start(chunk_start: int, target_tokens: int, dense_prefix_x: int = 4,

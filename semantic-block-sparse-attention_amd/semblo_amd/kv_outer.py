@@ -103,11 +103,32 @@ def kv_outer_attention(q: torch.Tensor, packed_kv: torch.Tensor, qmask: torch.Te
 
 class KVOuterPlan:
     """The reverse index of one chunk (kv_outer.py:254-329): everything the
-    attention needs from the selection, built before the one host read."""
+    attention needs from the selection, built before the one host read.  ``work``:
+    the chunk's work list and queue when ``prepare_work`` built them ahead, on the
+    plan's stream, with the partial capacity they were built for."""
 
     def __init__(self, qmask, nvis, qvals, counts, rev_indptr, nnz_d, qrank):
         self.qmask, self.nvis, self.qvals, self.counts = qmask, nvis, qvals, counts
         self.rev_indptr, self.nnz_d, self.qrank = rev_indptr, nnz_d, qrank
+        self.work = None
+
+    def prepare_work(self, q: torch.Tensor, hkv: int, bucket_indptr: torch.Tensor,
+                     guard: "PartialsGuard | None" = None) -> None:
+        """Build the work list ``kv_outer_execute`` would build for this chunk, with
+        its capacity bound (nothing is read on the host), on the current stream."""
+        qn, hq, d = q.shape
+        c = self.qmask.shape[2] * 32
+        cap, capped = partials_room(qn, hkv, c, hq // hkv, d, q.element_size(), guard)
+        items, queue = build_work_list(self, hkv, c, qn, queries_per_item(hq // hkv), bucket_indptr,
+                                       cap, capped, q.device)
+        self.work = (cap, capped, items, queue)
+
+    def tensors(self):
+        """The device tensors a chunk's execution reads (for record_stream)."""
+        t = [self.qmask, self.nvis, self.qvals, self.counts, self.rev_indptr, self.nnz_d, self.qrank]
+        if self.work is not None:
+            t += [self.work[2], self.work[3]]
+        return t
 
 
 def kv_outer_plan(qmask: torch.Tensor, causal_sizes: torch.Tensor, *, num_queries: int) -> KVOuterPlan:
@@ -194,6 +215,31 @@ class PartialsGuard:
         self.poll(wait=True)
 
 
+def partials_room(qn: int, hkv: int, c: int, g: int, d: int, elem_size: int,
+                  guard: PartialsGuard | None = None) -> tuple[int, bool]:
+    """(entries of the chunk's partial rows, capped): the capacity bound, capped at
+    ``partials_cap_bytes`` (or at the guard's room for the counts seen so far)."""
+    cap = partials_capacity(qn, hkv, c)
+    entry_bytes = g * d * elem_size + g * 4
+    limit = max(1, partials_cap_bytes() // entry_bytes)
+    if guard is not None:
+        limit = max(limit, guard.cap_entries)
+    return (limit, True) if cap > limit else (cap, False)
+
+
+def build_work_list(plan: KVOuterPlan, hkv: int, c: int, qn: int, qt: int, bucket_indptr: torch.Tensor,
+                    cap: int, capped: bool, dev):
+    """The chunk's work items (sbsa_prefill_items) and its claim queue, on the
+    current stream."""
+    bound = _lib.query("sbsa_prefill_items_bound", cap, qn, hkv, c, qt)
+    items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
+    queue = torch.empty(QUEUE_INTS, dtype=torch.int32, device=dev)
+    _lib.call("sbsa_prefill_items", _lib.ptr(plan.counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
+              _lib.ptr(plan.nvis), _lib.ptr(plan.rev_indptr), _lib.ptr(items), bound,
+              cap if capped else 0, _lib.ptr(queue), _lib.stream(dev))
+    return items, queue
+
+
 def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan, nnz: int | None,
                      bucket_indptr: torch.Tensor, *, sm_scale: float, local_kv, chunk_start: int,
                      wstart: int, out: torch.Tensor | None = None, want_stats: bool = False,
@@ -217,27 +263,21 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     if nnz is not None:
         cap = nnz
     else:
-        cap = partials_capacity(qn, hkv, c)
-        entry_bytes = g * d * q.element_size() + g * 4
-        limit = max(1, partials_cap_bytes() // entry_bytes)
-        if guard is not None:
-            limit = max(limit, guard.cap_entries)
-        if cap > limit:
-            cap, capped = limit, True
+        cap, capped = partials_room(qn, hkv, c, g, d, q.element_size(), guard)
     if out is None:
         out = torch.empty_like(q)
     part_o = torch.empty(max(cap, 1), g, d, dtype=q.dtype, device=dev)
     part_lse = torch.empty(max(cap, 1), g, dtype=torch.float32, device=dev)
     local_o = torch.empty_like(q)
     local_lse = torch.empty(qn, hq, dtype=torch.float32, device=dev)
-    qt = queries_per_item(g)
-    bound = _lib.query("sbsa_prefill_items_bound", cap, qn, hkv, c, qt)
-    items = torch.empty(max(bound, 1), ITEM_INTS, dtype=torch.int32, device=dev)
-    queue = torch.empty(QUEUE_INTS, dtype=torch.int32, device=dev)
     s = _lib.stream(dev)
-    _lib.call("sbsa_prefill_items", _lib.ptr(counts), hkv, c, qn, qt, 1, _lib.ptr(bucket_indptr),
-              _lib.ptr(nvis), _lib.ptr(rev_indptr), _lib.ptr(items), bound, cap if capped else 0,
-              _lib.ptr(queue), s)
+    if plan.work is not None and nnz is None and plan.work[:2] == (cap, capped):
+        # built ahead on the plan's stream (KVOuterPlan.prepare_work); used once
+        items, queue = plan.work[2], plan.work[3]
+        plan.work = None
+    else:
+        items, queue = build_work_list(plan, hkv, c, qn, queries_per_item(g), bucket_indptr, cap, capped,
+                                       dev)
     if timing is not None:
         timing.begin(s, "sparse")
     _lib.call("sbsa_prefill_attend", _lib.ptr(q), q.stride(0), q.stride(1), qn, hq, hkv, d,

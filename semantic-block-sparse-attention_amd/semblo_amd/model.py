@@ -217,6 +217,9 @@ class SembloAttention:
                                       iters=cfg.iters, dense_prefix_x=cfg.dense_prefix_x,
                                       keep_theta=self.plan_log is not None)
                 pl.record(self.plan_log)
+                # the chunk's work list too, here rather than on the main stream
+                # between two chunks' attention
+                pl.kv.prepare_work(q[st:en], index.num_kv_heads, index.bucket_indptr, guard)
                 ev = torch.cuda.Event()
                 ev.record(side)
             plans.append(pl)
