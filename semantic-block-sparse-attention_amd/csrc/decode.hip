@@ -116,24 +116,6 @@ size_t step_lds_bytes(int G, int C) {
   return sel > DecodeStep<D>::LDS_BYTES ? sel : DecodeStep<D>::LDS_BYTES;
 }
 
-// three independent integer sums over a wave, the same in every lane: rows of
-// 16 by DPP, the two halves by a lane swap, then two rows read out
-__device__ __forceinline__ void wave_sum3_i32_swap(int& x, int& y, int& z) {
-  x += dpp_i<0xB1>(x); y += dpp_i<0xB1>(y); z += dpp_i<0xB1>(z);
-  x += dpp_i<0x4E>(x); y += dpp_i<0x4E>(y); z += dpp_i<0x4E>(z);
-  x += dpp_i<0x124>(x); y += dpp_i<0x124>(y); z += dpp_i<0x124>(z);
-  x += dpp_i<0x128>(x); y += dpp_i<0x128>(y); z += dpp_i<0x128>(z);
-  const auto sx = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
-  const auto sy = __builtin_amdgcn_permlane32_swap((uint32_t)y, (uint32_t)y, false, false);
-  const auto sz = __builtin_amdgcn_permlane32_swap((uint32_t)z, (uint32_t)z, false, false);
-  x = (int)(sx[0] + sx[1]);
-  y = (int)(sy[0] + sy[1]);
-  z = (int)(sz[0] + sz[1]);
-  x = __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16);
-  y = __builtin_amdgcn_readlane(y, 0) + __builtin_amdgcn_readlane(y, 16);
-  z = __builtin_amdgcn_readlane(z, 0) + __builtin_amdgcn_readlane(z, 16);
-}
-
 // ------------------------------------------------------------- selection ---
 // All 256 threads.  NK = clusters per lane of wave 0 (C <= 64 NK).  Leaves
 // the CSR of the head's selection in s_rstart / s_rcum (rcount entries) and
@@ -349,9 +331,7 @@ __device__ __forceinline__ void select_phase(const DecodeArgs& a, int h, bool le
     live_total = wave_sum_i32_dpp(live_total);
     const float budget = (a.sink > 0) ? fmaxf(a.target - (float)a.sink, 0.f) : a.target;
     const bool all_fit = (float)live_total < budget;
-    // a count c (an integer below 2^24) reaches the budget when (float)c >= budget,
-    // that is when c >= ceil(budget)
-    const int bud_i = (int)ceilf(fminf(budget, 16777216.f));
+    const int bud_i = budget_count(budget);
     DPROBE(14);
     // two bisection steps per round: the first step's mid and both possible
     // second mids are counted together (the same fp32 mids as one step at a time)

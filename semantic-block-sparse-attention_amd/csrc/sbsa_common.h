@@ -152,6 +152,28 @@ __device__ __forceinline__ void wave_sum3_i32_dpp(int& x, int& y, int& z) {
   z = (__builtin_amdgcn_readlane(z, 0) + __builtin_amdgcn_readlane(z, 16)) +
       (__builtin_amdgcn_readlane(z, 32) + __builtin_amdgcn_readlane(z, 48));
 }
+// three independent integer sums over a wave, the same in every lane: rows of
+// 16 by DPP, the two halves by a lane swap, then two rows read out
+__device__ __forceinline__ void wave_sum3_i32_swap(int& x, int& y, int& z) {
+  x += dpp_i<0xB1>(x); y += dpp_i<0xB1>(y); z += dpp_i<0xB1>(z);
+  x += dpp_i<0x4E>(x); y += dpp_i<0x4E>(y); z += dpp_i<0x4E>(z);
+  x += dpp_i<0x124>(x); y += dpp_i<0x124>(y); z += dpp_i<0x124>(z);
+  x += dpp_i<0x128>(x); y += dpp_i<0x128>(y); z += dpp_i<0x128>(z);
+  const auto sx = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+  const auto sy = __builtin_amdgcn_permlane32_swap((uint32_t)y, (uint32_t)y, false, false);
+  const auto sz = __builtin_amdgcn_permlane32_swap((uint32_t)z, (uint32_t)z, false, false);
+  x = (int)(sx[0] + sx[1]);
+  y = (int)(sy[0] + sy[1]);
+  z = (int)(sz[0] + sz[1]);
+  x = __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16);
+  y = __builtin_amdgcn_readlane(y, 0) + __builtin_amdgcn_readlane(y, 16);
+  z = __builtin_amdgcn_readlane(z, 0) + __builtin_amdgcn_readlane(z, 16);
+}
+// the smallest integer count that reaches a budget: a count c below 2^24 (exact
+// in fp32) satisfies (float)c >= budget exactly when c >= ceil(budget)
+__device__ __forceinline__ int budget_count(float budget) {
+  return (int)ceilf(fminf(budget, 16777216.f));
+}
 // inclusive prefix sum over the wave (row scans by row_shr, then row carries)
 __device__ __forceinline__ int wave_incl_scan_dpp(int v) {
   v += dpp_i<0x111>(v);

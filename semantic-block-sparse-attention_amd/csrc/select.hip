@@ -32,7 +32,7 @@ struct SelectArgs {
   float inv_temp, beta, target;
 };
 
-template <int D>
+template <int D, int NK>
 __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) {
   constexpr int KS = D / 32;
   constexpr int LDQ = D + 8;
@@ -112,15 +112,17 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
     if (q >= a.Q) break;
     const int b = q / a.g_union;
     const int32_t* sz = a.sizes + (int64_t)b * a.s_nb + (int64_t)h * a.s_h;
-    float score[16], size[16];
-    float real_size[16];
+    float score[NK], size[NK];
+    float real_size[NK];
+    int size_i[NK];
     const int nk = C / 64;
     float hi = -INFINITY, lo = INFINITY;
     int live_total = 0;      // token counts: sizes sum to at most the prompt length
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < NK; ++k) {
       score[k] = NEG;
       size[k] = 0.f;
+      size_i[k] = 0;
       real_size[k] = 0.f;
       if (k < nk) {
         int c = lane + 64 * k;
@@ -131,6 +133,7 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
         float s = (a.sink > 0 && c == 0) ? 0.f : rs;  // the sink is hidden from the search
         real_size[k] = rs;
         size[k] = s;
+        size_i[k] = (int)s;
         bool live = s > 0.f;
         constexpr float LN2 = 0.69314718055994531f;
         float sc = __builtin_amdgcn_logf(fmaxf(p, 1e-38f)) * LN2;
@@ -149,6 +152,7 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
     float budget = a.target;
     if (a.sink > 0) budget = fmaxf(a.target - (float)a.sink, 0.f);
     const bool all_fit = (float)live_total < budget;
+    const int bud_i = budget_count(budget);
     // two bisection steps per round: the first step's mid and both possible
     // second mids are counted together (the same fp32 mids as one step at a time)
     for (int it = 0; it < a.iters; it += 2) {
@@ -157,24 +161,22 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
       const float m2 = (lo + m0) * 0.5f;     // second mid otherwise
       int c0 = 0, c1 = 0, c2 = 0;
 #pragma unroll
-      for (int k = 0; k < 16; ++k)
-        if (k < nk) {
-          const int sk = (int)size[k];
-          c0 += score[k] >= m0 ? sk : 0;
-          c1 += score[k] >= m1 ? sk : 0;
-          c2 += score[k] >= m2 ? sk : 0;
-        }
-      wave_sum3_i32_dpp(c0, c1, c2);
-      if ((float)c0 >= budget) {
+      for (int k = 0; k < NK; ++k) {         // size_i[k] is 0 past the C clusters
+        c0 += score[k] >= m0 ? size_i[k] : 0;
+        c1 += score[k] >= m1 ? size_i[k] : 0;
+        c2 += score[k] >= m2 ? size_i[k] : 0;
+      }
+      wave_sum3_i32_swap(c0, c1, c2);
+      if (c0 >= bud_i) {
         lo = m0;
         if (it + 1 < a.iters) {
-          if ((float)c1 >= budget) lo = m1;
+          if (c1 >= bud_i) lo = m1;
           else hi = m1;
         }
       } else {
         hi = m0;
         if (it + 1 < a.iters) {
-          if ((float)c2 >= budget) lo = m2;
+          if (c2 >= bud_i) lo = m2;
           else hi = m2;
         }
       }
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256) void score_select_kernel(SelectArgs a, int R) 
     int nsel = 0;
     int ntok = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < NK; ++k) {
       if (k < nk) {
         int c = lane + 64 * k;
         bool sel = (size[k] > 0.f && score[k] >= theta) || (a.sink > 0 && c == 0 && real_size[k] > 0.f);
@@ -469,6 +471,25 @@ __global__ __launch_bounds__(1024) void build_items_kernel(const int32_t* __rest
 
 }  // namespace
 
+// One instantiation per bound on the clusters a lane holds (C <= 64 NK).
+template <int D, int NK>
+int launch_select_nk(const SelectArgs& a, dim3 grid, size_t lds, int R, hipStream_t stream) {
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute((const void*)score_select_kernel<D, NK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return SBSA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((score_select_kernel<D, NK>), grid, dim3(256), lds, stream, a, R);
+  return SBSA_OK;
+}
+template <int D>
+int launch_select(const SelectArgs& a, dim3 grid, size_t lds, int R, hipStream_t stream) {
+  const int nk = a.C / 64;
+  if (nk <= 1) return launch_select_nk<D, 1>(a, grid, lds, R, stream);
+  if (nk <= 2) return launch_select_nk<D, 2>(a, grid, lds, R, stream);
+  if (nk <= 4) return launch_select_nk<D, 4>(a, grid, lds, R, stream);
+  return launch_select_nk<D, 16>(a, grid, lds, R, stream);
+}
+
 extern "C" {
 
 int sbsa_score_select(const void* vectors, int64_t v_sq, int64_t v_sh, const float* logmix,
@@ -522,26 +543,14 @@ int sbsa_score_select(const void* vectors, int64_t v_sq, int64_t v_sh, const flo
   dim3 grid((num_queries + QT - 1) / QT, num_kv_heads);
   size_t lds = (size_t)R * (dim + 8) * 2 + (size_t)R * (C + 1) * 4;
   if (lds > 160 * 1024) return SBSA_ERR_UNSUPPORTED;
-  if (lds > 64 * 1024) {
-    const void* fns[3] = {(const void*)score_select_kernel<64>, (const void*)score_select_kernel<128>,
-                          (const void*)score_select_kernel<256>};
-    for (const void* fn : fns)
-      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-        return SBSA_ERR_UNSUPPORTED;
-  }
+  int rc = SBSA_ERR_UNSUPPORTED;
   switch (dim) {
-    case 64:
-      hipLaunchKernelGGL(score_select_kernel<64>, grid, dim3(256), lds, stream, a, R);
-      break;
-    case 128:
-      hipLaunchKernelGGL(score_select_kernel<128>, grid, dim3(256), lds, stream, a, R);
-      break;
-    case 256:
-      hipLaunchKernelGGL(score_select_kernel<256>, grid, dim3(256), lds, stream, a, R);
-      break;
-    default:
-      return SBSA_ERR_UNSUPPORTED;
+    case 64: rc = launch_select<64>(a, grid, lds, R, stream); break;
+    case 128: rc = launch_select<128>(a, grid, lds, R, stream); break;
+    case 256: rc = launch_select<256>(a, grid, lds, R, stream); break;
+    default: break;
   }
+  if (rc) return rc;
   SBSA_CHECK_LAUNCH();
   return SBSA_OK;
 }
