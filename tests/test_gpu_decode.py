@@ -57,7 +57,12 @@ def _csr_to_sel(csr, idx):
 @pytest.mark.parametrize("cfg", [dict(length=4096, hq=16, hkv=4, d=256, seed=1),
                                  dict(length=3000, hq=8, hkv=2, d=128, seed=2),
                                  dict(length=2048, hq=8, hkv=1, d=128, seed=3),      # G = 8
-                                 dict(length=2048, hq=4, hkv=4, d=256, seed=4)])     # G = 1
+                                 dict(length=2048, hq=4, hkv=4, d=256, seed=4),      # G = 1
+                                 # two prompt splits and one suffix split per head and a large budget: each
+                                 # split takes its rows in two rounds (384 rows at D = 128,
+                                 # 192 at D = 256)
+                                 dict(length=4096, hq=8, hkv=2, d=128, seed=6, splits=2, suffix_splits=1, target=2048),
+                                 dict(length=4096, hq=16, hkv=4, d=256, seed=7, splits=2, suffix_splits=1, target=1024)])
 def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
     from semblo_amd.fused_decode import fused_decode_step
     from semblo_amd.synthetic import decode_queries
@@ -66,7 +71,8 @@ def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
     steps = 40
     qs, kn, vn = decode_queries(inp, steps, hq, seed=cfg["seed"])
     layer = _Layer(hq, hkv, d)
-    target = length // 16
+    target = cfg.get("target", length // 16)
+    splits = cfg.get("splits", 16)
     c = idx.num_buckets
     csr = torch.empty(3 * hkv * c + 2 * hkv, dtype=torch.int32, device=DEV)
     out = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
@@ -78,8 +84,8 @@ def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
         q = qs[t:t + 1].to(DEV)
         fused_decode_step(layer, arena, q_post=q, q_pre=q, positions=pos, k_post=kn[t:t + 1].to(DEV),
                           v_states=vn[t:t + 1].to(DEV), output=out, temperature=0.1, beta=0.25,
-                          target_tokens=target, sm_scale=d ** -0.5, num_splits=16, iters=16,
-                          out_lse=lse, csr_out=csr)
+                          target_tokens=target, sm_scale=d ** -0.5, num_splits=splits, iters=16,
+                          suffix_splits=cfg.get("suffix_splits"), out_lse=lse, csr_out=csr)
         torch.cuda.synchronize()
         sel = _csr_to_sel(csr.cpu(), idx)
         want = ref.decode_reference(q[0].cpu(), packed, idx.bucket_indptr.cpu(),
