@@ -673,10 +673,11 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs a) {
 // Block (query head, 64 dimensions); wave w sums splits w, w+4, ... of its 64
 // dims.  The partials are loaded first; every wave derives the splits' common
 // maximum and scales itself (no block barrier before the sums).
-template <int D>
+template <int D, int PS>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) {
   constexpr int PRE = 16;                 // splits per wave loaded up front
-  __shared__ float s_sc[4][MAX_SPLITS];
+  // PS: splits per lane of the maxima and sums (S <= 64 PS)
+  __shared__ float s_sc[4][64 * PS];
   __shared__ float s_red[4][64];
   const int hq = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -693,7 +694,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int S) 
   }
   const float* pm = a.pm + (int64_t)hq * S;
   const float* pl = a.pl + (int64_t)hq * S;
-  constexpr int PS = MAX_SPLITS / 64;
   float pmv[PS], plv[PS];
 #pragma unroll
   for (int k = 0; k < PS; ++k) {
@@ -748,7 +748,10 @@ int launch_step(const DecodeArgs& a, hipStream_t stream) {
   }
   const int S = a.nsplit + a.ssplit;
   hipLaunchKernelGGL((decode_step_kernel<D, G, NK>), dim3(a.Hkv, S), dim3(256), lds, stream, a);
-  hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
+  if (S <= 64)
+    hipLaunchKernelGGL((decode_merge_kernel<D, 1>), dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
+  else
+    hipLaunchKernelGGL((decode_merge_kernel<D, MAX_SPLITS / 64>), dim3(a.Hq, D / 64), dim3(256), 0, stream, a, S);
   return SBSA_OK;
 }
 
