@@ -17,11 +17,14 @@
 //      the CSR to the workspace and the token's K/V into the suffix store.
 //      A head's keys are one list, the selected prompt rows in CSR order
 //      followed by the live suffix rows (the current token's row read from
-//      k_new/v_new); each split takes an even, 32-aligned range of it.  The
-//      block resolves its rows' addresses into LDS, each wave gathers 32-key
-//      tiles straight into LDS (global loads to LDS) and runs S^T = K Q^T and
-//      O^T = V^T P^T on MFMA with the G query heads as columns; the waves'
-//      partials are folded in LDS into the split's partial.
+//      k_new/v_new); each split takes an even, 32-aligned range of it, in
+//      rounds of RC rows.  Per round the block resolves the rows' addresses
+//      into LDS; each wave loads the K rows of its 16-key groups straight into
+//      registers and runs S^T = K Q^T on MFMA with the G query heads as
+//      columns, while every wave copies a share of the V rows into LDS
+//      (global loads to LDS).  P goes through LDS, and each wave accumulates
+//      O^T = V^T P^T for its own D/4 dimensions over all the round's keys, so
+//      the split's partial is written with no fold across waves.
 //   2. merge: one block per (query head, 64 dimensions) folds the splits.
 #include "sbsa_common.h"
 
