@@ -174,7 +174,6 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
   static_assert(EPI_STORES <= 63, "vmcnt range");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem_attn[];
   __shared__ int s_items[2];
-  __shared__ int s_over[4];         // pass 0: a row of wave w passed the overflow bound
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar LDS bases
@@ -629,10 +628,6 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
     };
     // the general form, for the tiles around a wave's last active one; with
     // sweep set it only tracks the rows' maxima (no probabilities, no O)
-    // pass 0: whether a row of the wave passed the overflow bound, published in
-    // LDS before the barrier of the item's last step (every row's sum is final
-    // there), so that every wave reads all four after it with no barrier of its own
-    bool check_overflow = false;
     auto step = [&](int t, f32x16_t& cur, f32x16_t& nxt, bool sweep) {
       const bool staged = issue_next(t);
       const bool act = t * KT <= wave_lim;
@@ -646,11 +641,6 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
       if (act && !sweep) {
         exp_pack(cur, pb);
         gemm_pv(pb, vbuf_at(t & 1));
-      }
-      if (check_overflow && t == ntiles - 1) {
-        const float l = halves_sum(l_part);
-        const int over = __builtin_amdgcn_readfirstlane(__ballot(!(l <= __builtin_exp2f(OVERFLOW_LOG2))) != 0);
-        if (lane == 0) s_over[wave] = over;
       }
       finish_step(staged);
     };
@@ -692,7 +682,6 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         const float mx = halves_max(lmax_all);
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
       }
-      check_overflow = pass == 0;
       int t = 0;
       if (!sweep) {
         // tiles 0..t_last hold keys some row of this wave may see; the steady
@@ -708,9 +697,9 @@ __global__ __launch_bounds__(256, 1) void attn_items_kernel(AttnArgs a) {
         if (t + 1 < ntiles) step(t + 1, sB, sA, sweep);
       }
       if (pass == 0) {
-        // the last step's barrier has made every wave's flag visible
-        check_overflow = false;
-        if (!(s_over[0] | s_over[1] | s_over[2] | s_over[3])) break;
+        const float l = halves_sum(l_part);
+        const bool over = !(l <= __builtin_exp2f(OVERFLOW_LOG2));
+        if (!__syncthreads_or(over ? 1 : 0)) break;
       } else if (sweep) {
         const float mx = halves_max(lmax_all);
         m_ref = (mx == NEG_INF) ? 0.f : mx * a.scale_log2;
