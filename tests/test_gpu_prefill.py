@@ -209,3 +209,29 @@ def test_dense_chunk_redone_when_a_key_towers_over_the_first_tile(beta):
     want = attention_reference(q[cs:ce + 1], keys, k, v, d ** -0.5)
     err = assert_close_bf16(out, want, f"towering key, beta {beta}")
     print(f"beta {beta}: max err {err:.3g}")
+
+
+def test_layer_prefill_is_bit_identical_across_reruns():
+    """The work items are claimed in whatever order the blocks reach the queue,
+    and every item writes its own partial rows: the same prompt must give the
+    same bits on every run.  A missing barrier between an item's last tile and
+    the next item's loads showed up here as one wave's rows differing in about
+    one run in sixteen, so the layer is run 24 times."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.model import SembloAttention
+    from semblo_amd.synthetic import mixture_layer
+    length, hq, hkv, d = 4096, 8, 2, 128
+    inp = mixture_layer(length, hq, hkv, d, mixtures=32, seed=11)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    outs = []
+    for i in range(24):
+        cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=512,
+                                  codebook_seed=3, layer_idx=0)
+        layer = SembloAttention(cfg, layer_name=f"rerun.{i}")
+        out = torch.empty(length, hq * d, dtype=torch.bfloat16, device=DEV)
+        layer.prefill(q.view(length, -1), q.view(length, -1), k, k, v, out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs[1:], 1):
+        rows = (out != outs[0]).any(1).nonzero().flatten()
+        assert rows.numel() == 0, f"run {i}: rows {rows[:16].tolist()} differ from run 0"
