@@ -8,6 +8,7 @@ sanitizer.  The emulation's lane models are pinned to a probe run on an MI355X
 the GPU tests check them, at small sizes.  CPU only."""
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
@@ -18,6 +19,10 @@ sys.path.insert(0, str(HERE / "emu"))
 
 pytestmark = pytest.mark.emu
 CASES = str(HERE / "emu" / "cases.py")
+# the cases that take a minute or more each run only with SBSA_EMU_LONG=1, so that
+# the default CPU suite stays at a few minutes
+long_case = pytest.mark.skipif(os.environ.get("SBSA_EMU_LONG", "0") != "1",
+                               reason="long emulated case: set SBSA_EMU_LONG=1")
 
 
 def _run(case, *args, **kw):
@@ -54,10 +59,12 @@ def test_emulated_dense_prefix_chunk():
     _run("dense_chunk", 256, 8, 2, 128, 128, 191, 3)
 
 
+@long_case
 def test_emulated_sparse_chunk():
     _run("sparse_chunk", 1024, 8, 2, 128, 512, 767, 1, 2)
 
 
+@long_case
 def test_emulated_decode_steps():
     _run("decode_steps", 1024, 8, 2, 128, 5)
 
@@ -68,6 +75,7 @@ def test_emulated_decode_steps_in_several_rounds():
     _run("decode_steps", 1024, 4, 1, 256, 7, 1, 1, 512)
 
 
+@long_case
 def test_gpu_selection_and_append_tests_under_emulation():
     """The selection tests and the token-order append tests, run unchanged on the
     emulated kernels (each kernel's every memory access under the sanitizer)."""
@@ -76,6 +84,7 @@ def test_gpu_selection_and_append_tests_under_emulation():
          "test_gpu_token_order.py::test_append_rows_flags_an_id_out_of_range", timeout=900)
 
 
+@long_case
 def test_kmeans_build_with_restarts_under_emulation():
     """The index build on keys that leave clusters empty (restarts drawn ahead and
     applied on the device, then on the host past two), run unchanged on the emulated
