@@ -8,6 +8,12 @@ Mirrors the reference's SembloAttention paths that the operator reaches
   _run_product_attention   the query-chunk loop                               (model.py:856-1008)
   _full_graph_decode_step  the decode step over the arena                     (model.py:708-783)
   begin_token_outer_prefill  a token-order prefill session   (token_outer_prefill.py:127-212)
+  begin_streamed_prefill     a layer-major streamed prefill session   (model.py:1271-1279)
+
+The projections around the attention (Q/K/V with RoPE and the output gate and
+projection) belong to the model, which is not part of this build.  A model that
+drives the streamed sessions with hidden states, as the reference's streamer
+does, attaches them with ``attach_projections``.
 
 vLLM's metadata, paged cache and profiling branch are not part of this
 build: the layer keeps its own per-request state, and a call with more than
@@ -57,7 +63,66 @@ class SembloAttention:
         self.target_tokens = 0
         # test hook: a list here receives every sparse chunk's selection (ChunkPlan.record)
         self.plan_log: list | None = None
+        self._projections = None
         register_layer(self.layer_name, self)
+
+    # -- the model's projections (attached by the caller) -------------------------
+    def attach_projections(self, project_qkv, finish_output, project_kv=None) -> None:
+        """The model's side of the layer, for the sessions driven by hidden states.
+
+        ``project_qkv(rope_positions, hidden_states)`` returns (q_post, k_post, v,
+        q_pre, k_pre, gate): Q and K after and before the rotary embedding, V, and
+        the output gate or None (the reference's model ``_project_qkv``,
+        qwen3_5_model.py:135, nemotron_h_model.py:149).  ``finish_output(attn, gate)``
+        takes the attention [n, Hq*D] to the layer's output (``_finish_output``,
+        qwen3_5_model.py:225-235).  ``project_kv`` returns (k_post, v, k_pre) alone; by
+        default the full projection runs and Q is dropped (model.py:356-368)."""
+        self._projections = (project_qkv, finish_output, project_kv)
+
+    def _require_projections(self):
+        if self._projections is None:
+            raise RuntimeError(f"layer {self.layer_name!r} has no projections: a session driven by "
+                               "hidden states needs attach_projections(project_qkv, finish_output)")
+        return self._projections
+
+    def _project_qkv(self, rope_positions, hidden_states):
+        return self._require_projections()[0](rope_positions, hidden_states)
+
+    def _project_kv(self, rope_positions, hidden_states):
+        project_qkv, _, project_kv = self._require_projections()
+        if project_kv is not None:
+            return project_kv(rope_positions, hidden_states)
+        _q, k_post, v, _qp, k_pre, _g = project_qkv(rope_positions, hidden_states)
+        return k_post, v, k_pre
+
+    def _finish_output(self, attn: torch.Tensor, gate):
+        return self._require_projections()[1](attn, gate)
+
+    @staticmethod
+    def _positions_for_runtime(positions: torch.Tensor):
+        """(rotary positions, flat positions): an M-RoPE grid [3, T] keeps its first row
+        as the flat one (qwen3_5_model.py:124-133)."""
+        if positions.ndim == 2:
+            return positions, positions[0]
+        return positions, positions
+
+    @staticmethod
+    def _slice_positions(rope_positions: torch.Tensor, start: int, stop: int) -> torch.Tensor:
+        """Rows [start, stop) of the rotary positions, [T] or [3, T] (model.py:1290-1299)."""
+        if rope_positions.ndim == 2:
+            return rope_positions[:, start:stop]
+        return rope_positions[start:stop]
+
+    def _prompt_positions(self, tokens_or_positions):
+        """(tokens, rotary positions or None) of a new prompt given as a length or as its
+        positions, which must be 0 .. T-1: the index holds one prompt from position 0."""
+        if not isinstance(tokens_or_positions, torch.Tensor):
+            return int(tokens_or_positions), None
+        rope, flat = self._positions_for_runtime(tokens_or_positions)
+        tokens = int(flat.numel())
+        if not torch.equal(flat.reshape(-1).to("cpu", torch.int64), torch.arange(tokens)):
+            raise ValueError("a prompt's positions must run 0 .. T-1 (one prompt, from its start)")
+        return tokens, rope
 
     # -- routing (S0) ---------------------------------------------------------
     def _query_state(self, q_pre: torch.Tensor) -> SembloQueryState:
@@ -91,19 +156,23 @@ class SembloAttention:
             self._side_stream = st
         return st
 
-    def begin_token_outer_prefill(self, tokens: int, chunk: int, **kw):
-        """A token-order prefill session of ``tokens`` positions in slices of ``chunk``
-        (the reference's layer.begin_token_outer_prefill, streamed_prefill.py:563-564)."""
+    def begin_token_outer_prefill(self, tokens, chunk: int, **kw):
+        """A token-order prefill session of a prompt (its length, or its positions as
+        the reference passes them) in slices of ``chunk`` (the reference's
+        layer.begin_token_outer_prefill, model.py:1281, streamed_prefill.py:563-564)."""
         from .token_outer_prefill import TokenOuterPrefillSession
+        tokens, rope = self._prompt_positions(tokens)
         self.index = None
         self.arena = None
-        return TokenOuterPrefillSession(self, tokens, chunk, **kw)
+        return TokenOuterPrefillSession(self, tokens, chunk, rope_positions=rope, **kw)
 
-    def begin_streamed_prefill(self, tokens: int):
-        """This layer's share of a layer-major streamed prefill of ``tokens`` positions:
-        ``keys`` for every slice, then ``ingest``, then ``queries`` for every slice
-        (the reference's layer.begin_streamed_prefill, model.py:1271-1279)."""
+    def begin_streamed_prefill(self, tokens):
+        """This layer's share of a layer-major streamed prefill of a prompt (its length,
+        or its positions as the reference passes them): ``keys`` for every slice, then
+        ``ingest``, then ``queries`` for every slice (the reference's
+        layer.begin_streamed_prefill, model.py:1271-1279)."""
         from .streamed_prefill import StreamedPrefillSession
+        tokens, _rope = self._prompt_positions(tokens)
         return StreamedPrefillSession(self, tokens)
 
     def prefill_streamed(self, q_post, q_pre, k_pre, k_post, v, output, slice_tokens: int,
@@ -115,13 +184,13 @@ class SembloAttention:
         spans = [(s, min(length, s + slice_tokens)) for s in range(0, length, slice_tokens)]
         session = self.begin_streamed_prefill(length)
         for st, en in spans:
-            session.keys(k_pre.view(length, hkv, d)[st:en], k_post.view(length, hkv, d)[st:en],
-                         v.view(length, hkv, d)[st:en], st, en)
+            session.stage_keys(k_pre.view(length, hkv, d)[st:en], k_post.view(length, hkv, d)[st:en],
+                               v.view(length, hkv, d)[st:en], st, en)
         session.ingest()
         out = output.view(length, hq, d)
         for st, en in spans:
-            session.queries(q_post.view(length, hq, d)[st:en], q_pre.view(length, hq, d)[st:en], st,
-                            out=out[st:en], timing=timing)
+            session.attend(q_post.view(length, hq, d)[st:en], q_pre.view(length, hq, d)[st:en], st,
+                           out=out[st:en], timing=timing)
         session.finish()
         return output
 
@@ -152,10 +221,12 @@ class SembloAttention:
         out = output.view(length, hq, d)
         for start in range(0, length, chunk):
             stop = min(length, start + chunk)
-            session.slice(q_post.view(length, hq, d)[start:stop], q_pre.view(length, hq, d)[start:stop],
-                          k_pre.view(length, hkv, d)[start:stop], k_post.view(length, hkv, d)[start:stop],
-                          v.view(length, hkv, d)[start:stop], start, stop, out=out[start:stop],
-                          timing=timing, store_timing=store_timing)
+            session.slice_projected(q_post.view(length, hq, d)[start:stop],
+                                    q_pre.view(length, hq, d)[start:stop],
+                                    k_pre.view(length, hkv, d)[start:stop],
+                                    k_post.view(length, hkv, d)[start:stop],
+                                    v.view(length, hkv, d)[start:stop], start, stop, out=out[start:stop],
+                                    timing=timing, store_timing=store_timing)
         self.last_session = session
         session.finish()
         return output

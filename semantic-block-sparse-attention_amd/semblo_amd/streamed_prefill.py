@@ -17,9 +17,13 @@ model.py:1431-1531), which its ``PrefillStreamer`` drives slice by slice
   finish   the index becomes the layer's decode state.
 
 With slices that are a multiple of the chunk size the chunks are those of the
-whole-prompt path, and so are the outputs, bit for bit.  This build has no
-model to project hidden states, so ``keys`` and ``queries`` take the layer's
-projections of the slice, as the token-order session does.
+whole-prompt path, and so are the outputs, bit for bit.
+
+``keys(rope_positions, hidden_states, start, stop)`` and ``queries(rope_positions,
+positions, hidden_states, start)`` are the reference's calls: they run the
+projections the model attached to the layer (``SembloAttention.attach_projections``)
+and ``queries`` returns the layer's output rows.  ``stage_keys`` and ``attend`` take
+the projections themselves, for a caller that has them already.
 """
 from __future__ import annotations
 
@@ -50,9 +54,18 @@ class StreamedPrefillSession:
         layer.arena = None
 
     # -- pass 1 -----------------------------------------------------------------
-    def keys(self, k_pre: torch.Tensor, k_post: torch.Tensor, v: torch.Tensor, start: int,
+    def keys(self, rope_positions: torch.Tensor, hidden_states: torch.Tensor, start: int,
              stop: int) -> None:
-        """Stage positions [start, stop): k_pre, k_post, v [n, Hkv, D] (model.py:1465-1491)."""
+        """Project positions [start, stop) with the layer's projections and stage their
+        K/V and pre-RoPE keys (model.py:1463-1491)."""
+        k_post, v, k_pre = self.layer._project_kv(rope_positions, hidden_states)
+        if k_post is None or v is None or k_pre is None:
+            raise RuntimeError("the streamed prefill needs a layer with its own K/V")
+        self.stage_keys(k_pre, k_post, v, start, stop)
+
+    def stage_keys(self, k_pre: torch.Tensor, k_post: torch.Tensor, v: torch.Tensor, start: int,
+                   stop: int) -> None:
+        """Stage positions [start, stop): k_pre, k_post, v [n, Hkv, D] (model.py:1481-1491)."""
         if self.index is not None:
             raise RuntimeError("keys after ingest: the index is already fitted")
         layer = self.layer
@@ -86,8 +99,22 @@ class StreamedPrefillSession:
         self.k_pre = self.k_post = self.v = None
 
     # -- pass 2 -----------------------------------------------------------------
-    def queries(self, q_post: torch.Tensor, q_pre: torch.Tensor, start: int,
-                out: torch.Tensor | None = None, timing=None) -> torch.Tensor:
+    def queries(self, rope_positions: torch.Tensor, positions: torch.Tensor,
+                hidden_states: torch.Tensor, start: int) -> torch.Tensor:
+        """The layer's output rows for the slice at ``start``: its queries projected with
+        the layer's projections, attended, then gated and projected out
+        (model.py:1509-1524).  ``positions`` are the slice's flat positions (start ..
+        start+n-1; only their count is checked, so that nothing waits for the GPU)."""
+        layer = self.layer
+        n = int(hidden_states.shape[0])
+        if positions.numel() != n:
+            raise ValueError(f"{positions.numel()} positions for {n} hidden rows")
+        q_post, _k, _v, q_pre, _kp, gate = layer._project_qkv(rope_positions, hidden_states)
+        attn = self.attend(q_post, q_pre, start)
+        return layer._finish_output(attn.view(n, -1), gate)
+
+    def attend(self, q_post: torch.Tensor, q_pre: torch.Tensor, start: int,
+               out: torch.Tensor | None = None, timing=None) -> torch.Tensor:
         """The attention of positions start..start+n-1 (q_post, q_pre [n, Hq, D]) into
         ``out`` [n, Hq, D] (model.py:1509-1524, 856-1000)."""
         if self.index is None:

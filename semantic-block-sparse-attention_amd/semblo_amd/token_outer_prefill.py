@@ -150,16 +150,22 @@ class TokenOuterSnapshot:
 class TokenOuterPrefillSession:
     """One sparse layer's share of a token-order prefill (token_outer_prefill.py:127-400).
 
-    ``slice`` takes the layer's projections of positions [start, stop) --
-    q_post [n, Hq, D], q_pre [n, Hq, D], k_pre, k_post, v [n, Hkv, D] -- where
-    the reference's ``slice(hidden_states, start, stop)`` projects them
-    itself; slices must come in order and cover the prompt.
+    ``slice(hidden_states, start, stop)`` is the reference's call: it projects the
+    slice with the projections the model attached to the layer
+    (``SembloAttention.attach_projections``) and returns the layer's output rows.
+    ``slice_projected`` takes the projections of positions [start, stop) instead --
+    q_post [n, Hq, D], q_pre [n, Hq, D], k_pre, k_post, v [n, Hkv, D].  Slices must
+    come in order and cover the prompt.
     """
 
-    def __init__(self, layer, tokens: int, chunk: int, *, fit_tokens: int | None = None) -> None:
+    def __init__(self, layer, tokens: int, chunk: int, *, fit_tokens: int | None = None,
+                 rope_positions: torch.Tensor | None = None) -> None:
         cfg = layer.runtime_config
         self.layer = layer
         self.tokens = int(tokens)
+        # the rotary positions [T] or [3, T] the reference's session slices for its
+        # projections; None: 0 .. T-1 on the hidden states' device
+        self.rope_positions = rope_positions
         self.chunk = int(chunk)
         if self.chunk > int(cfg.query_chunk_size):
             raise RuntimeError(
@@ -194,8 +200,26 @@ class TokenOuterPrefillSession:
         self._reserve_dev = staged.to(device, non_blocking=True)
 
     # -- per slice ------------------------------------------------------------------
-    def slice(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
-              out: torch.Tensor | None = None, timing=None, store_timing=None) -> torch.Tensor:
+    def slice(self, hidden_states: torch.Tensor, start: int, stop: int) -> torch.Tensor:
+        """The layer's output rows for positions [start, stop): the slice projected with
+        the layer's projections, its keys appended, its queries attended, then gated and
+        projected out (token_outer_prefill.py:173-196)."""
+        layer = self.layer
+        n = int(stop) - int(start)
+        if int(hidden_states.shape[0]) != n:
+            raise ValueError(f"{hidden_states.shape[0]} hidden rows for the slice [{start}, {stop})")
+        if self.rope_positions is None:
+            rope = torch.arange(int(start), int(stop), device=hidden_states.device)
+        else:
+            rope = layer._slice_positions(self.rope_positions, int(start), int(stop))
+        q_post, k_post, v, q_pre, k_pre, gate = layer._project_qkv(rope, hidden_states)
+        if k_post is None or v is None or k_pre is None:
+            raise RuntimeError("the token-outer prefill needs a layer with its own K/V")
+        attn = self.slice_projected(q_post, q_pre, k_pre, k_post, v, start, stop)
+        return layer._finish_output(attn.view(n, -1), gate)
+
+    def slice_projected(self, q_post, q_pre, k_pre, k_post, v, start: int, stop: int,
+                        out: torch.Tensor | None = None, timing=None, store_timing=None) -> torch.Tensor:
         """Attention of positions [start, stop) into ``out`` [n, Hq, D].  ``timing``
         brackets the attention launches, ``store_timing`` the store kernels of an
         append (assignment, rows, K/V writes), each with HIP events."""

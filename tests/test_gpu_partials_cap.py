@@ -71,8 +71,8 @@ def test_token_order_prefill_is_the_same_under_a_tiny_cap(monkeypatch):
         out = torch.empty(tokens, 8, 128, dtype=torch.bfloat16, device=DEV)
         for start in range(0, tokens, chunk):
             stop = min(tokens, start + chunk)
-            session.slice(q[start:stop], q[start:stop], k[start:stop], k[start:stop], v[start:stop],
-                          start, stop, out=out[start:stop])
+            session.slice_projected(q[start:stop], q[start:stop], k[start:stop], k[start:stop], v[start:stop],
+                                    start, stop, out=out[start:stop])
         session.finish()
         torch.cuda.synchronize()
         outs.append(out.cpu())

@@ -181,8 +181,8 @@ def _run_session(cfg, k_override=None):
     for start in range(0, tokens, chunk):
         stop = min(tokens, start + chunk)
         appended = session.index is not None or start >= session.fit_at
-        session.slice(q[start:stop], q[start:stop], k[start:stop], k[start:stop], v[start:stop],
-                      start, stop, out=out[start:stop])
+        session.slice_projected(q[start:stop], q[start:stop], k[start:stop], k[start:stop], v[start:stop],
+                                start, stop, out=out[start:stop])
         if appended:
             # the ids the session appended with (same kernel, same input)
             ids_by_slice[start] = nearest_cluster(k[start:stop], session.index.codebooks).cpu()

@@ -58,4 +58,34 @@ def test_streamed_queries_refuse_a_slice_past_the_prompt():
     q = torch.zeros(8, 4, 64, dtype=torch.bfloat16)
     for start in (95, -1, 100):
         with pytest.raises(ValueError, match="outside the prompt"):
-            session.queries(q, q, start)
+            session.attend(q, q, start)
+
+
+def test_sessions_driven_by_hidden_states_need_projections_and_a_prompt_from_zero():
+    """A session driven by hidden states runs the model's projections, which the
+    model attaches to the layer: without them it refuses.  Positions given to
+    begin_* must run 0 .. T-1, as a [T] row or an M-RoPE grid [3, T]."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.model import SembloAttention
+    cfg = SembloRuntimeConfig(num_q_heads=4, num_kv_heads=1, head_dim=64)
+    layer = SembloAttention(cfg, layer_name="host.hidden")
+    session = layer.begin_streamed_prefill(torch.arange(256))
+    assert session.tokens == 256
+    with pytest.raises(RuntimeError, match="no projections"):
+        session.keys(torch.arange(0, 64), torch.zeros(64, 32), 0, 64)
+    grid = torch.arange(300).expand(3, 300)
+    assert layer.begin_streamed_prefill(grid).tokens == 300
+    token = layer.begin_token_outer_prefill(grid, 64)
+    assert token.tokens == 300 and token.rope_positions.shape == (3, 300)
+    with pytest.raises(RuntimeError, match="no projections"):
+        token.slice(torch.zeros(64, 32), 0, 64)
+    with pytest.raises(ValueError, match="0 .. T-1"):
+        layer.begin_streamed_prefill(torch.arange(5, 261))
+    rope, flat = layer._positions_for_runtime(grid)
+    assert rope is grid and torch.equal(flat, torch.arange(300))
+    assert torch.equal(layer._slice_positions(grid, 10, 20), grid[:, 10:20])
+    calls = []
+    layer.attach_projections(lambda p, h: calls.append(("qkv", p)) or (None,) * 6, lambda a, g: a)
+    with pytest.raises(RuntimeError, match="its own K/V"):
+        session.keys(torch.arange(0, 64), torch.zeros(64, 32), 0, 64)
+    assert calls and calls[0][0] == "qkv"
