@@ -235,3 +235,82 @@ def test_layer_prefill_is_bit_identical_across_reruns():
     for i, out in enumerate(outs[1:], 1):
         rows = (out != outs[0]).any(1).nonzero().flatten()
         assert rows.numel() == 0, f"run {i}: rows {rows[:16].tolist()} differ from run 0"
+
+
+def _synthetic_runs(seed, *, hkv, g, d, clusters=64, qn=48, n_local=56, page=16, empty_head=None):
+    """A chunk over synthetic page-multiple cluster runs, after the reference's own
+    synthetic case (tests/test_kv_outer_fused_local.py:86-106): run sizes 1-16 pages,
+    visible rows anywhere from none to the whole run, random selections of which three
+    queries pick nothing in KV head 1, and optionally a KV head with no cluster at all.
+    The window holds n_local >= qn rows, as every query sees itself."""
+    gen = torch.Generator().manual_seed(seed)
+    sizes = torch.randint(1, 17, (clusters,), generator=gen) * page
+    length = int(sizes.sum())
+    indptr = torch.zeros(hkv, clusters + 1, dtype=torch.int32)
+    indptr[:, 1:] = torch.cumsum(sizes, 0)[None].to(torch.int32)
+    causal = (torch.rand(hkv, clusters, generator=gen) * (sizes[None] + 1)).floor()
+    causal = torch.minimum(causal, sizes[None].float()).to(torch.int32)
+    qmask = torch.randint(0, 1 << 31, (qn, hkv, clusters // 32), generator=gen, dtype=torch.int64)
+    qmask = (qmask & torch.randint(0, 1 << 31, qmask.shape, generator=gen)).to(torch.int32)
+    qmask[:3, 1] = 0
+    if empty_head is not None:
+        qmask[:, empty_head] = 0
+    packed = torch.randn(2, length, hkv, d, generator=gen).to(torch.bfloat16)
+    q = torch.randn(qn, hkv * g, d, generator=gen).to(torch.bfloat16)
+    local = torch.randn(2, n_local, hkv, d, generator=gen).to(torch.bfloat16)
+    return q, packed, qmask, causal, indptr, local
+
+
+def _synthetic_reference(q, packed, qmask, causal, indptr, local, wstart, chunk_start):
+    """fp64 attention of each query over its selected clusters' first causal rows and
+    the window rows up to its own position."""
+    qn = q.shape[0]
+    hkv, c = causal.shape
+    length, n_local = packed.shape[1], local.shape[1]
+    sel = ref.unpack_bits(qmask, c)                                   # [Q, Hkv, C]
+    run = torch.zeros(hkv, c, length, dtype=torch.bool)
+    for h in range(hkv):
+        for ci in range(c):
+            a = int(indptr[h, ci])
+            run[h, ci, a:a + int(causal[h, ci])] = True
+    keys_run = torch.einsum("qhc,hcl->qhl", sel.double(), run.double()) > 0
+    own = chunk_start + torch.arange(qn) - wstart                     # window row of each query
+    keys_win = (torch.arange(n_local)[None, :] <= own[:, None])[:, None, :].expand(qn, hkv, n_local)
+    keys = torch.cat([keys_run, keys_win], -1)
+    k = torch.cat([packed[0], local[0]], 0)
+    v = torch.cat([packed[1], local[1]], 0)
+    return attention_reference(q, keys, k, v, q.shape[-1] ** -0.5)
+
+
+@pytest.mark.parametrize("hkv,g,d,empty_head", [(2, 2, 128, None), (2, 2, 128, 0), (4, 4, 256, 2)])
+def test_kv_outer_on_synthetic_runs_with_empty_selections(hkv, g, d, empty_head):
+    """Cluster runs of ragged page counts, visible rows from none to all, queries and a
+    whole KV head selecting nothing: every row within bf16 tolerance of fp64 over the
+    defined key set, and a query that selected nothing in a head gets exactly the
+    window's attention (the same bits as a run in which no query selects anything)."""
+    from semblo_amd.kv_outer import kv_outer_attention
+    q, packed, qmask, causal, indptr, local = _synthetic_runs(11 + hkv, hkv=hkv, g=g, d=d,
+                                                              empty_head=empty_head)
+    qn, n_local = q.shape[0], local.shape[1]
+    wstart, chunk_start = 1000, 1000 + n_local - qn
+
+    def run(mask):
+        out, _ = kv_outer_attention(q.to(DEV), packed.to(DEV), mask.to(DEV), causal.to(DEV),
+                                    indptr.to(DEV), sm_scale=d ** -0.5,
+                                    local_kv=(local[0].to(DEV), local[1].to(DEV)),
+                                    chunk_start=chunk_start, wstart=wstart)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    got = run(qmask)
+    want = _synthetic_reference(q, packed, qmask, causal, indptr, local, wstart, chunk_start)
+    assert torch.isfinite(got.float()).all()
+    assert_close_bf16(got, want, "synthetic runs")
+    window_only = run(torch.zeros_like(qmask))
+    assert_close_bf16(window_only, _synthetic_reference(q, packed, torch.zeros_like(qmask), causal,
+                                                        indptr, local, wstart, chunk_start), "window")
+    none = ~ref.unpack_bits(qmask, causal.shape[1]).any(-1)           # [Q, Hkv]: selected nothing
+    assert bool(none[:3, 1].all())
+    for h in range(hkv):
+        rows = none[:, h].nonzero().flatten()
+        assert torch.equal(got[rows, h * g:(h + 1) * g], window_only[rows, h * g:(h + 1) * g]), h
