@@ -107,7 +107,7 @@ def decode_graph(layer, inp, steps, cfg):
     pos = torch.arange(length, length + steps, dtype=torch.int32, device="cuda")
     outs = torch.empty(steps, hq * d, dtype=torch.bfloat16, device="cuda")
     kw = dict(temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
-              target_tokens=layer.target_tokens, sm_scale=layer.scaling,
+              target_tokens=layer.decode_budget(), sm_scale=layer.scaling,
               num_splits=cfg.decode_num_splits, iters=cfg.iters,
               suffix_splits=cfg.decode_suffix_splits)
 

@@ -14,6 +14,15 @@ the block table maps every block a generation can reach onto the suffix store
 as a ring (arena.py:186-202): a flush frees the oldest blocks and the blocks
 that follow take them.  The decode step then reads the prompt length from
 ``prompt_length_t`` on the device, which a flush advances.
+
+``DecodeArena.with_capacity`` makes an arena before any request, shaped for a
+prompt capacity and a fixed cluster count (arena.py:66-160, vLLM's FULL graph
+mode): a decode step captured on it at warm-up replays for every later request,
+because ``adopt`` copies each request's index into the same buffers.  Clusters
+past the request's own have size 0, an empty run and a zero descriptor, so no
+selection reaches them (their zero scores still count in each component's
+log-sum-exp, as in the reference's arena); the suffix table is rewritten for the
+request's prompt length, and the step reads that length on the device.
 """
 from __future__ import annotations
 
@@ -92,8 +101,108 @@ class DecodeArena:
     @property
     def reads_prompt_length_on_device(self) -> bool:
         """The decode step takes the prompt length from ``prompt_length_t`` (a flush
-        moves it); without the flush it is the host value, known at capture."""
-        return self.flush_room > 0
+        moves it, an adoption sets it); otherwise it is the host value, known at capture."""
+        return self.flush_room > 0 or self.capacity is not None
+
+    capacity: int | None = None     # set by with_capacity: the arena outlives its requests
+
+    @classmethod
+    def with_capacity(cls, *, capacity: int, num_kv_heads: int, head_dim: int, num_clusters: int,
+                      page_align: int = 16, reserve: int = 1024, suffix_block: int = 256,
+                      suffix_splits: int = 8, dtype=torch.bfloat16, device="cuda") -> "DecodeArena":
+        """An arena for prompts of up to ``capacity`` positions and ``num_clusters``
+        clusters, made before any request (arena.py:66-130).  Until the first ``adopt``
+        it holds a one-token index (cluster 0 of every head holds position 0, the other
+        clusters are empty), so a step captured on it reads finite, zero K/V.  The suffix
+        flush does not run on such an arena."""
+        self = cls.__new__(cls)
+        dev = torch.device(device)
+        hkv, d, c = int(num_kv_heads), int(head_dim), int(num_clusters)
+        self.capacity = int(capacity)
+        self.num_clusters = c
+        self.page_align = max(int(page_align), 1)
+        self.reserve = int(reserve)
+        self.suffix_block = int(suffix_block)
+        self.suffix_splits = int(suffix_splits)
+        self.flush_room = 0
+        tile = 16
+        self.max_tiles = -(-self.reserve // tile)
+        bs = self.suffix_block
+        width = self.capacity + c * self.page_align
+        width += (-width) % PACK_ALIGN
+        self.codebooks = torch.zeros(hkv, 2, c, d // 2, dtype=dtype, device=dev)
+        self.sizes = torch.zeros(hkv, c, dtype=torch.int32, device=dev)
+        self.indptr = torch.zeros(hkv, c + 1, dtype=torch.int32, device=dev)
+        self.packed_kv = torch.zeros(2, width, hkv, d, dtype=dtype, device=dev)
+        self.posting = torch.zeros(hkv, width, dtype=torch.int32, device=dev)
+        self.inverse = None
+        self.suffix_kpre_needed = False
+        # positions L .. L + reserve - 1 of any prompt length L <= capacity span at most
+        # reserve / bs + 2 blocks
+        self.suffix_blocks = -(-self.reserve // bs) + 2
+        self.suffix_kv = torch.zeros(2, self.suffix_blocks, bs, hkv, d, dtype=dtype, device=dev)
+        self.suffix_kpre = None
+        span = self.capacity + self.max_tiles * tile
+        self.suffix_table = torch.zeros(span // bs + 2, dtype=torch.int32, device=dev)
+        self.prompt_length_t = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.spare = None
+        self.flushes = 0
+        self.steps = 0
+        self.index = None
+        # the one-token index, with the prompt length at the capacity (arena.py:116-121)
+        self.sizes[:, 0] = 1
+        self.indptr[:, 1:] = 1
+        self._map_suffix(self.capacity)
+        return self
+
+    def _map_suffix(self, prompt_length: int) -> None:
+        """Blocks from the one holding the prompt's end onward map onto the suffix store
+        in order, and the step reads the new prompt length."""
+        bs = self.suffix_block
+        base = int(prompt_length) // bs
+        n = self.suffix_table.numel()
+        table = torch.zeros(n, dtype=torch.int32)
+        blocks = torch.arange(base, n)
+        table[base:] = ((blocks - base) % self.suffix_blocks).to(torch.int32)
+        self.suffix_table.copy_(table)
+        self.prompt_length = int(prompt_length)
+        self.first_prompt_length = int(prompt_length)
+        self.prompt_length_t.fill_(int(prompt_length))
+
+    def adopt(self, index) -> None:
+        """Copy a request's finished index into this capacity arena (arena.py:160-253):
+        every buffer keeps its address, so a step captured before the request replays
+        over it.  Refuses an index larger than the arena."""
+        if self.capacity is None:
+            raise RuntimeError("adopt is for an arena made with_capacity")
+        hkv, c = index.bucket_sizes.shape
+        length = int(index.prompt_length)
+        packed = index.packed_kv
+        if packed is None:
+            raise ValueError("the arena needs the index's packed K/V (pack_prompt_kv)")
+        if hkv != self.sizes.shape[0] or packed.shape[3] != self.packed_kv.shape[3]:
+            raise ValueError(f"index of {hkv} KV heads x D={packed.shape[3]} for an arena of "
+                             f"{self.sizes.shape[0]} x D={self.packed_kv.shape[3]}")
+        if c > self.num_clusters:
+            raise ValueError(f"the index has {c} clusters; the arena holds {self.num_clusters}")
+        if length > self.capacity:
+            raise ValueError(f"a prompt of {length} positions; the arena holds {self.capacity}")
+        rows = packed.shape[1]
+        if rows > self.packed_kv.shape[1]:
+            raise ValueError(f"{rows} packed rows; the arena holds {self.packed_kv.shape[1]}")
+        self.codebooks.zero_()
+        self.codebooks[:, :, :c].copy_(index.codebooks)
+        self.sizes.zero_()
+        self.sizes[:, :c].copy_(index.bucket_sizes)
+        self.indptr[:, :c + 1].copy_(index.bucket_indptr)
+        self.indptr[:, c + 1:] = index.bucket_indptr[:, c:c + 1]
+        self.packed_kv[:, :rows].copy_(packed)
+        npost = index.posting_positions.shape[1]
+        self.posting[:, :npost].copy_(index.posting_positions)
+        self._map_suffix(length)
+        self.spare = None
+        self.steps = 0
+        self.index = index
 
     def suffix_rows(self, positions: torch.Tensor, kv_head: int):
         """K and V of the generated tokens at ``positions`` (host helper for tests)."""

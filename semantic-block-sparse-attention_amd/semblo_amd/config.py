@@ -87,6 +87,14 @@ class SembloRuntimeConfig:
     sm_scale: float | None = None           # None: head_dim ** -0.5
     suffix_shuffle_seed: int | None = None  # suffix blocks in a shuffled physical order (a paged
                                             # cache's page order); None: in order
+    decode_capacity: int = 0                # > 0: one decode arena for prompts up to this length,
+                                            # made before any request and adopted into by each
+                                            # (SEMBLO_FULL_GRAPH_DECODE, arena.py:66-253); the
+                                            # decode budget is then budget(decode_capacity)
+    # decode's own budget (SEMBLO_DECODE_TARGET_TOKENS, config.py:262-268 of the reference);
+    # 0: decode selects on the prefill's budget.  The prompt length reads every cluster.
+    decode_target_tokens: int = field(default_factory=lambda: int(
+        os.environ.get("SEMBLO_DECODE_TARGET_TOKENS", "0") or 0))
 
     @property
     def scale(self) -> float:

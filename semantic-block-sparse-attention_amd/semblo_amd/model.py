@@ -64,6 +64,7 @@ class SembloAttention:
         # test hook: a list here receives every sparse chunk's selection (ChunkPlan.record)
         self.plan_log: list | None = None
         self._projections = None
+        self._capacity_arena: DecodeArena | None = None
         register_layer(self.layer_name, self)
 
     # -- the model's projections (attached by the caller) -------------------------
@@ -194,11 +195,49 @@ class SembloAttention:
         session.finish()
         return output
 
+    def capacity_arena(self, device) -> DecodeArena:
+        """The layer's fixed-address decode arena for prompts of up to
+        ``decode_capacity`` positions, made on first use (before any request, for a
+        caller that captures the decode step at warm-up); its cluster count is the rule's
+        at the capacity (arena.py:43-48)."""
+        cfg = self.runtime_config
+        if cfg.decode_capacity <= 0:
+            raise RuntimeError("the layer has no decode capacity (decode_capacity = 0)")
+        if self._capacity_arena is None:
+            from .config import num_flat_clusters
+            self._capacity_arena = DecodeArena.with_capacity(
+                capacity=cfg.decode_capacity, num_kv_heads=self.num_kv_heads, head_dim=self.head_dim,
+                num_clusters=num_flat_clusters(cfg.decode_capacity, cfg.flat_unit_tokens,
+                                               cfg.flat_min_clusters_log2),
+                page_align=cfg.page_align, reserve=cfg.suffix_reserve, suffix_block=cfg.suffix_block,
+                suffix_splits=cfg.decode_suffix_splits, device=device)
+        return self._capacity_arena
+
+    def decode_budget(self) -> int:
+        """The selection budget of a decode step, chosen per step (model.py:847-854):
+        ``decode_target_tokens`` when set, else with a capacity arena the budget at the
+        capacity (the one a step captured before the request was made with), else the
+        last prefill's budget.  A later prefill sets its own again."""
+        cfg = self.runtime_config
+        if cfg.decode_target_tokens > 0:
+            return int(cfg.decode_target_tokens)
+        if cfg.decode_capacity > 0:
+            return cfg.budget(cfg.decode_capacity)
+        return int(self.target_tokens)
+
     def adopt_index(self, index: ProductPostingIndex) -> None:
         """Make a finished prompt index the layer's decode state."""
         cfg = self.runtime_config
         index.original_kv = None
         self.index = index
+        if cfg.decode_capacity > 0:
+            if suffix_flush.flush_every() > 0:
+                raise RuntimeError("the suffix flush does not run on a fixed-capacity decode arena "
+                                   "(decode_capacity > 0)")
+            arena = self.capacity_arena(index.packed_kv.device)
+            arena.adopt(index)
+            self.arena = arena
+            return
         shuffle = None if cfg.suffix_shuffle_seed is None else \
             torch.Generator().manual_seed(int(cfg.suffix_shuffle_seed))
         every = suffix_flush.flush_every()
@@ -349,7 +388,7 @@ class SembloAttention:
         fused_decode_step(self, self.arena, q_post=q_post, q_pre=q_pre, positions=positions,
                           k_post=k_post, v_states=v, k_pre=k_pre, output=output,
                           temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
-                          target_tokens=self.target_tokens, sm_scale=self.scaling,
+                          target_tokens=self.decode_budget(), sm_scale=self.scaling,
                           num_splits=cfg.decode_num_splits, iters=cfg.iters,
                           suffix_splits=cfg.decode_suffix_splits)
         return output

@@ -126,7 +126,7 @@ def _decode_checks(layer, inp, steps, tag, seed=1, graph_replay=False):
     outs = torch.empty(steps, hq * d, dtype=torch.bfloat16, device=DEV)
     csr = torch.empty(3 * hkv * c + 2 * hkv, dtype=torch.int32, device=DEV)
     kw = dict(temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
-              target_tokens=layer.target_tokens, sm_scale=layer.scaling,
+              target_tokens=layer.decode_budget(), sm_scale=layer.scaling,
               num_splits=cfg.decode_num_splits, iters=cfg.iters, suffix_splits=arena.suffix_splits)
     codebooks, sizes, indptr = idx.codebooks.cpu(), idx.bucket_sizes.cpu(), idx.bucket_indptr.cpu()
     near = 0
@@ -139,7 +139,7 @@ def _decode_checks(layer, inp, steps, tag, seed=1, graph_replay=False):
         q_cpu = qs[t].cpu()
         exp = oracle_select(ref.trivial_router_vectors(q_cpu[None], 1), codebooks, sizes[None],
                             temperature=cfg.selection_temperature, beta=cfg.bucket_size_penalty,
-                            target=layer.target_tokens)
+                            target=layer.decode_budget())
         near += compare_selection(sel[None], exp["sel"], exp["score"], exp["theta"])["near_ties"]
         want = decode_rows_reference(q_cpu, idx.packed_kv, indptr, sizes, sel, kn[:t + 1].cpu(),
                                      vn[:t + 1].cpu(), layer.scaling)

@@ -62,7 +62,12 @@ def _csr_to_sel(csr, idx):
                                  # split takes its rows in two rounds (384 rows at D = 128,
                                  # 192 at D = 256)
                                  dict(length=4096, hq=8, hkv=2, d=128, seed=6, splits=2, suffix_splits=1, target=2048),
-                                 dict(length=4096, hq=16, hkv=4, d=256, seed=7, splits=2, suffix_splits=1, target=1024)])
+                                 dict(length=4096, hq=16, hkv=4, d=256, seed=7, splits=2, suffix_splits=1, target=1024),
+                                 # a budget of the whole prompt selects every live cluster: the
+                                 # reference's dense decode case (tests/test_dense_prompt_decode.py),
+                                 # here through the same step
+                                 dict(length=2048, hq=8, hkv=2, d=128, seed=8, target=2048),
+                                 dict(length=1000, hq=16, hkv=4, d=256, seed=9, target=4096)])
 def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
     from semblo_amd.fused_decode import fused_decode_step
     from semblo_amd.synthetic import decode_queries
@@ -88,10 +93,15 @@ def test_decode_steps_match_fp64_over_selection_and_suffix(cfg):
                           suffix_splits=cfg.get("suffix_splits"), out_lse=lse, csr_out=csr)
         torch.cuda.synchronize()
         sel = _csr_to_sel(csr.cpu(), idx)
-        want = ref.decode_reference(q[0].cpu(), packed, idx.bucket_indptr.cpu(),
-                                    idx.bucket_sizes.cpu(), sel, kn[:t + 1].cpu(), vn[:t + 1].cpu(),
-                                    d ** -0.5)
+        want, want_lse = ref.decode_reference(q[0].cpu(), packed, idx.bucket_indptr.cpu(),
+                                              idx.bucket_sizes.cpu(), sel, kn[:t + 1].cpu(),
+                                              vn[:t + 1].cpu(), d ** -0.5, with_lse=True)
         assert_close_bf16(out.view(hq, d).cpu(), want, f"step {t}")
+        # natural-log LSE of the scaled scores, the merge's convention; the reference's
+        # tolerance (tests/test_dense_prompt_decode.py:64)
+        torch.testing.assert_close(lse.cpu().double(), want_lse, atol=2e-3, rtol=1e-4)
+        if target >= length:
+            assert torch.equal(sel, idx.bucket_sizes.cpu() > 0), "a whole-prompt budget selects every cluster"
         vec = ref.trivial_router_vectors(q.cpu(), 1)
         exp = oracle_select(vec, idx.codebooks.cpu(), idx.bucket_sizes.cpu()[None],
                             temperature=0.1, beta=0.25, target=target)
@@ -177,3 +187,89 @@ def test_layer_decode_refuses_a_step_past_the_suffix_reserve():
     pos = torch.tensor([length + reserve], dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="suffix_reserve"):
         layer.decode(pos, qs[-1:].to(DEV), qs[-1:].to(DEV), kn[-1:].to(DEV), vn[-1:].to(DEV), dec)
+
+
+def _csr_to_arena_sel(csr, arena):
+    """[Hkv, C_arena] bool: the clusters of the arena whose runs the step's CSR names."""
+    hkv, c = arena.sizes.shape
+    n = hkv * c
+    rstart = csr[:n].view(hkv, c)
+    rcount = csr[3 * n:3 * n + hkv]
+    indptr, sizes = arena.indptr.cpu(), arena.sizes.cpu()
+    sel = torch.zeros(hkv, c, dtype=torch.bool)
+    for h in range(hkv):
+        for p in range(int(rcount[h])):
+            cand = torch.nonzero((indptr[h, :-1] == int(rstart[h, p])) & (sizes[h] > 0)).flatten()
+            assert cand.numel() == 1
+            sel[h, cand[0]] = True
+    return sel
+
+
+def test_capacity_arena_step_captured_before_any_request_replays_for_each():
+    """vLLM's FULL graph mode (arena.py:1-27 of the reference): the step is captured
+    once, on a capacity-shaped arena holding a one-token index, before any request.
+    Each request's index is then adopted into the same buffers (one with fewer clusters
+    than the arena: its tail clusters are empty, with zero descriptors), and the same
+    graph, fed through fixed input buffers, runs every step: the same bits as the step
+    run eagerly, fp64 attention over the CSR's clusters and the suffix, natural-log LSE,
+    and the selection of the oracle over the arena's padded descriptors and sizes."""
+    from semblo_amd.arena import DecodeArena
+    from semblo_amd.fused_decode import fused_decode_step
+    from semblo_amd.state import ProductPostingIndex
+    from semblo_amd.synthetic import decode_queries, mixture_layer
+    hq, hkv, d, cap, ncl, target = 8, 2, 128, 4096, 128, 256
+    layer = _Layer(hq, hkv, d)
+    arena = DecodeArena.with_capacity(capacity=cap, num_kv_heads=hkv, head_dim=d, num_clusters=ncl,
+                                      reserve=512, suffix_splits=4, device=DEV)
+    bf = torch.bfloat16
+    qb = torch.zeros(1, hq, d, dtype=bf, device=DEV)
+    kb = torch.zeros(1, hkv, d, dtype=bf, device=DEV)
+    vb = torch.zeros(1, hkv, d, dtype=bf, device=DEV)
+    pos = torch.full((1,), cap, dtype=torch.int32, device=DEV)
+    out = torch.empty(1, hq * d, dtype=bf, device=DEV)
+    lse = torch.empty(hq, dtype=torch.float32, device=DEV)
+    csr = torch.empty(3 * hkv * ncl + 2 * hkv, dtype=torch.int32, device=DEV)
+
+    def step():
+        fused_decode_step(layer, arena, q_post=qb, q_pre=qb, positions=pos, k_post=kb, v_states=vb,
+                          output=out, temperature=0.1, beta=0.25, target_tokens=target,
+                          sm_scale=d ** -0.5, num_splits=16, iters=16, out_lse=lse, csr_out=csr)
+
+    step()                                   # warm-up on the one-token index: makes the workspace
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for length, seed, min_log2 in ((3000, 21, 3), (2048, 22, 7)):
+        inp = mixture_layer(length, hq, hkv, d, mixtures=32, seg=(32, 256), seed=seed)
+        k, v = inp.k.to(DEV), inp.v.to(DEV)
+        idx = ProductPostingIndex.build(k, torch.arange(length, device=DEV), codebook_seed=seed,
+                                        router_pass=True, flat_min_clusters_log2=min_log2)
+        idx.pack_prompt_kv(k, v)
+        assert idx.num_buckets <= ncl
+        arena.adopt(idx)
+        assert int(arena.prompt_length_t.item()) == length
+        qs, kn, vn = decode_queries(inp, 6, hq, seed=seed)
+        for t in range(6):
+            qb.copy_(qs[t:t + 1].to(DEV))
+            kb.copy_(kn[t:t + 1].to(DEV))
+            vb.copy_(vn[t:t + 1].to(DEV))
+            pos.fill_(length + t)
+            graph.replay()
+            torch.cuda.synchronize()
+            got, got_lse, got_csr = out.clone(), lse.clone(), csr.clone()
+            step()                            # the same step, eagerly
+            torch.cuda.synchronize()
+            assert torch.equal(got, out) and torch.equal(got_lse, lse) and torch.equal(got_csr, csr)
+            sel = _csr_to_arena_sel(got_csr.cpu(), arena)
+            assert not bool(sel[:, idx.num_buckets:].any())
+            want, want_lse = ref.decode_reference(qs[t].cpu(), arena.packed_kv.cpu(), arena.indptr.cpu(),
+                                                  arena.sizes.cpu(), sel, kn[:t + 1].cpu(), vn[:t + 1].cpu(),
+                                                  d ** -0.5, with_lse=True)
+            assert_close_bf16(got.view(hq, d).cpu(), want, f"L={length} step {t}")
+            torch.testing.assert_close(got_lse.cpu().double(), want_lse, atol=2e-3, rtol=1e-4)
+            vec = ref.trivial_router_vectors(qs[t:t + 1].cpu(), 1)
+            exp = oracle_select(vec, arena.codebooks.cpu(), arena.sizes.cpu()[None], temperature=0.1,
+                                beta=0.25, target=target)
+            compare_selection(sel[None], exp["sel"], exp["score"], exp["theta"])

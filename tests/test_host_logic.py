@@ -89,3 +89,79 @@ def test_sessions_driven_by_hidden_states_need_projections_and_a_prompt_from_zer
     with pytest.raises(RuntimeError, match="its own K/V"):
         session.keys(torch.arange(0, 64), torch.zeros(64, 32), 0, 64)
     assert calls and calls[0][0] == "qkv"
+
+
+def test_capacity_arena_adopts_in_place_with_empty_tail_clusters():
+    """DecodeArena.with_capacity / adopt on CPU tensors (arena.py:66-253 of the
+    reference): before any request a one-token index with the prompt length at the
+    capacity; an adopted index fills the first clusters, the rest are empty runs with
+    zero descriptors, the suffix table maps the blocks from the prompt's end, and no
+    buffer moves.  An index larger than the arena is refused."""
+    import types
+    from semblo_amd.arena import DecodeArena
+    hkv, d, cap, ncl = 2, 8, 1000, 16
+    arena = DecodeArena.with_capacity(capacity=cap, num_kv_heads=hkv, head_dim=d, num_clusters=ncl,
+                                      reserve=300, suffix_block=64, dtype=torch.float32, device="cpu")
+    assert arena.reads_prompt_length_on_device and int(arena.prompt_length_t) == cap
+    assert arena.sizes[:, 0].tolist() == [1, 1] and int(arena.sizes[:, 1:].sum()) == 0
+    assert arena.indptr[:, 1:].eq(1).all()
+    ptrs = [t.data_ptr() for t in (arena.codebooks, arena.sizes, arena.indptr, arena.packed_kv,
+                                   arena.suffix_kv, arena.suffix_table, arena.prompt_length_t)]
+    c, length = 5, 700
+    sizes = torch.tensor([[100, 0, 300, 250, 50], [140, 140, 140, 140, 140]], dtype=torch.int32)
+    padded = (sizes + 15) // 16 * 16
+    indptr = torch.zeros(hkv, c + 1, dtype=torch.int32)
+    indptr[:, 1:] = padded.cumsum(1)
+    rows = int(indptr[:, -1].max()) + 40
+    index = types.SimpleNamespace(
+        bucket_sizes=sizes, bucket_indptr=indptr, prompt_length=length,
+        codebooks=torch.randn(hkv, 2, c, d // 2), packed_kv=torch.randn(2, rows, hkv, d),
+        posting_positions=torch.randint(0, length, (hkv, rows), dtype=torch.int32))
+    arena.adopt(index)
+    assert [t.data_ptr() for t in (arena.codebooks, arena.sizes, arena.indptr, arena.packed_kv,
+                                   arena.suffix_kv, arena.suffix_table, arena.prompt_length_t)] == ptrs
+    assert torch.equal(arena.sizes[:, :c], sizes) and int(arena.sizes[:, c:].abs().sum()) == 0
+    assert torch.equal(arena.indptr[:, :c + 1], indptr)
+    assert torch.equal(arena.indptr[:, c + 1:], indptr[:, c:c + 1].expand(hkv, ncl - c))
+    assert torch.equal(arena.codebooks[:, :, :c], index.codebooks)
+    assert int(arena.codebooks[:, :, c:].abs().sum()) == 0
+    assert torch.equal(arena.packed_kv[:, :rows], index.packed_kv)
+    assert int(arena.prompt_length_t) == length and arena.prompt_length == length
+    # positions 700 .. 999 (the reserve) land in distinct physical blocks from block 10 on
+    blocks = torch.arange(length, length + 300) // 64
+    phys = arena.suffix_table[blocks]
+    assert phys[0] == 0 and len(set(phys.tolist())) == int(blocks[-1] - blocks[0]) + 1
+    assert int(phys.max()) < arena.suffix_kv.shape[1]
+    assert int(arena.suffix_table[:length // 64].abs().sum()) == 0
+    big = types.SimpleNamespace(**{**vars(index), "prompt_length": cap + 1})
+    with pytest.raises(ValueError, match="arena holds 1000"):
+        arena.adopt(big)
+    many = types.SimpleNamespace(**{**vars(index), "bucket_sizes": torch.ones(hkv, ncl + 1, dtype=torch.int32)})
+    with pytest.raises(ValueError, match="clusters"):
+        arena.adopt(many)
+
+
+def test_decode_budget_is_chosen_per_step(monkeypatch):
+    """Decode selects on its own budget when SEMBLO_DECODE_TARGET_TOKENS sets one
+    (tests/test_decode_only_budget.py of the reference), else on the last prefill's,
+    else with a capacity arena on the budget at the capacity; a prefill's budget is
+    left as it was (model.py:847-854)."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.model import SembloAttention
+    monkeypatch.delenv("SEMBLO_DECODE_TARGET_TOKENS", raising=False)
+    cfg = SembloRuntimeConfig(num_q_heads=4, num_kv_heads=1, head_dim=64)
+    assert cfg.decode_target_tokens == 0
+    layer = SembloAttention(cfg, layer_name="host.budget.a")
+    layer.target_tokens = cfg.budget(65536)            # what a prefill of 65536 sets
+    assert layer.decode_budget() == 4096
+    monkeypatch.setenv("SEMBLO_DECODE_TARGET_TOKENS", "524288")
+    cfg = SembloRuntimeConfig(num_q_heads=4, num_kv_heads=1, head_dim=64)
+    layer = SembloAttention(cfg, layer_name="host.budget.b")
+    layer.target_tokens = cfg.budget(65536)
+    assert layer.decode_budget() == 524288
+    assert layer.target_tokens == 4096, "the prefill keeps its budget"
+    monkeypatch.delenv("SEMBLO_DECODE_TARGET_TOKENS")
+    cfg = SembloRuntimeConfig(num_q_heads=4, num_kv_heads=1, head_dim=64, decode_capacity=131072)
+    layer = SembloAttention(cfg, layer_name="host.budget.c")
+    layer.target_tokens = cfg.budget(2048)
+    assert layer.decode_budget() == 8192
