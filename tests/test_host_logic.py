@@ -165,3 +165,25 @@ def test_decode_budget_is_chosen_per_step(monkeypatch):
     layer = SembloAttention(cfg, layer_name="host.budget.c")
     layer.target_tokens = cfg.budget(2048)
     assert layer.decode_budget() == 8192
+
+
+def test_flush_range_keeps_the_newest_and_moves_the_rest():
+    """suffix_flush.flush_range (suffix_flush.py:140-152 of the reference), the cases of
+    its own test: once the exact suffix holds keep + every tokens, everything but the
+    newest ``keep`` moves, from the current prompt length on; an empty range moves
+    nothing."""
+    from semblo_amd.suffix_flush import flush_layer, flush_range
+    length, keep, every = 1000, 100, 50
+    plen, moved = length, []
+    for written in range(400):
+        assert length + written - plen < keep + every + 1
+        r = flush_range(length, written, plen, keep, every)
+        if r is not None:
+            frm, to = r
+            assert frm == plen and to == length + written - keep and to - frm >= every
+            moved.append(r)
+            plen = to
+    assert moved and moved[0] == (length, length + 50)
+    assert all(b - a == every for a, b in moved)
+    assert flush_range(length, 10 ** 6, length, keep, 0) is None          # flush off
+    assert flush_layer(object(), 1200, 1200) == 0                         # nothing to move
