@@ -273,3 +273,54 @@ def test_capacity_arena_step_captured_before_any_request_replays_for_each():
             exp = oracle_select(vec, arena.codebooks.cpu(), arena.sizes.cpu()[None], temperature=0.1,
                                 beta=0.25, target=target)
             compare_selection(sel[None], exp["sel"], exp["score"], exp["theta"])
+
+
+def test_layer_decodes_two_requests_on_its_capacity_arena():
+    """A layer with decode_capacity keeps one arena across requests: each prefill's index
+    is adopted into it (here 64 clusters into an arena of 128), nothing moves, and the
+    layer's decode steps select on the capacity budget rule (an explicit target here):
+    the same bits as the step run directly, fp64 over the CSR's clusters and the suffix."""
+    from semblo_amd.config import SembloRuntimeConfig
+    from semblo_amd.fused_decode import fused_decode_step
+    from semblo_amd.model import SembloAttention
+    from semblo_amd.synthetic import decode_queries, mixture_layer
+    hq, hkv, d = 8, 2, 128
+    cfg = SembloRuntimeConfig(num_q_heads=hq, num_kv_heads=hkv, head_dim=d, query_chunk_size=512,
+                              target_tokens=256, flat_min_clusters_log2=3, decode_capacity=262144,
+                              suffix_reserve=64)
+    layer = SembloAttention(cfg, layer_name="test.decode.capacity")
+    arena = layer.capacity_arena(DEV)
+    assert arena.num_clusters == 128
+    ptrs = [t.data_ptr() for t in (arena.codebooks, arena.sizes, arena.indptr, arena.packed_kv,
+                                   arena.suffix_kv, arena.suffix_table)]
+    assert layer.decode_budget() == 256
+    c = arena.num_clusters
+    csr = torch.empty(3 * hkv * c + 2 * hkv, dtype=torch.int32, device=DEV)
+    for length, seed in ((4096, 31), (2048, 32)):
+        inp = mixture_layer(length, hq, hkv, d, mixtures=16, seed=seed)
+        q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+        out = torch.empty(length, hq * d, dtype=torch.bfloat16, device=DEV)
+        layer.prefill(q, q, k, k, v, out)
+        assert layer.arena is arena and layer.index.num_buckets == 64
+        assert [t.data_ptr() for t in (arena.codebooks, arena.sizes, arena.indptr, arena.packed_kv,
+                                       arena.suffix_kv, arena.suffix_table)] == ptrs
+        qs, kn, vn = decode_queries(inp, 5, hq, seed=seed)
+        dec = torch.empty(1, hq * d, dtype=torch.bfloat16, device=DEV)
+        again = torch.empty_like(dec)
+        for t in range(5):
+            pos = torch.tensor([length + t], dtype=torch.int32, device=DEV)
+            qt, kt, vt = qs[t:t + 1].to(DEV), kn[t:t + 1].to(DEV), vn[t:t + 1].to(DEV)
+            layer.decode(pos, qt, qt, kt, vt, dec)
+            fused_decode_step(layer, arena, q_post=qt, q_pre=qt, positions=pos, k_post=kt, v_states=vt,
+                              output=again, temperature=cfg.selection_temperature,
+                              beta=cfg.bucket_size_penalty, target_tokens=layer.decode_budget(),
+                              sm_scale=layer.scaling, num_splits=cfg.decode_num_splits, iters=cfg.iters,
+                              suffix_splits=cfg.decode_suffix_splits, csr_out=csr)
+            torch.cuda.synchronize()
+            assert torch.equal(dec, again)
+            sel = _csr_to_arena_sel(csr.cpu(), arena)
+            assert not bool(sel[:, 64:].any())
+            want = ref.decode_reference(qs[t].cpu(), arena.packed_kv.cpu(), arena.indptr.cpu(),
+                                        arena.sizes.cpu(), sel, kn[:t + 1].cpu(), vn[:t + 1].cpu(),
+                                        d ** -0.5)
+            assert_close_bf16(dec.view(hq, d).cpu(), want, f"L={length} step {t}")
