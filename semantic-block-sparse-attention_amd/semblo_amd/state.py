@@ -50,13 +50,13 @@ class _DrawBuffers:
 
     def __init__(self, length: int, fit_n: int, c: int):
         self.sub = torch.empty(fit_n, dtype=torch.int64)        # a host-side restart's draw
-        # a head's draws: sample permutation, init rows, restart rows drawn ahead
-        self.perm = torch.empty(length, dtype=torch.int64)
-        self.init = torch.empty(fit_n, dtype=torch.int64)
-        self.restarts = torch.empty(RESTARTS_AHEAD, fit_n, dtype=torch.int64)
+        # a head's draws (sample permutation, init rows, restart rows drawn ahead), in
+        # two sets: the next head's are drawn ahead into the set the current head is not using
+        self.sets = [_HeadDraws(length, fit_n) for _ in range(2)]
         self.pinned = torch.empty(fit_n + (1 + RESTARTS_AHEAD) * c, dtype=torch.int32,
                                   pin_memory=True)
         self.uploaded = None            # event after the last upload from `pinned`
+        self.last_empties = 0           # empty k-means iterations of the last head fitted
         self.counts = None              # pinned [iterations, C] cluster counts
 
     def counts_host(self, iters: int, c: int) -> torch.Tensor:
@@ -67,7 +67,26 @@ class _DrawBuffers:
         return self.counts[:iters]
 
 
+class _HeadDraws:
+    """One KV head's permutations on the host."""
+
+    def __init__(self, length: int, fit_n: int):
+        self.perm = torch.empty(length, dtype=torch.int64)
+        self.init = torch.empty(fit_n, dtype=torch.int64)
+        self.restarts = torch.empty(RESTARTS_AHEAD, fit_n, dtype=torch.int64)
+
+
 _DRAW_BUFFERS: dict = {}
+_DRAW_AHEAD = None          # the worker thread that draws the next KV head's permutations ahead
+DRAW_AHEAD_STATS = {"used": 0, "discarded": 0}
+
+
+def _draw_ahead_pool():
+    global _DRAW_AHEAD
+    if _DRAW_AHEAD is None:
+        from concurrent.futures import ThreadPoolExecutor
+        _DRAW_AHEAD = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sbsa-draws")
+    return _DRAW_AHEAD
 
 
 def _draw_buffers(length: int, fit_n: int, c: int) -> _DrawBuffers:
@@ -214,29 +233,38 @@ class ProductPostingIndex:
 
         k_ahead = RESTARTS_AHEAD
 
-        def draw():
+        def draws(g, hd):
             """fit_flat_codebook's first two draws (flat_index.py:237-262), then the
             draws of the first k_ahead restarts (flat_index.py:277-283) made ahead: the
             GPU applies the k-th at the k-th iteration that leaves a cluster empty.
             Returns the generator's state before each restart draw, to take back the
-            draws no iteration needs, and uploads the draws from pinned memory."""
-            torch.randperm(n_fit, generator=gen, out=host.perm)
-            torch.randperm(fit_n, generator=gen, out=host.init)
+            draws no iteration needs."""
+            torch.randperm(n_fit, generator=g, out=hd.perm)
+            torch.randperm(fit_n, generator=g, out=hd.init)
             before = []
             for k in range(k_ahead):
-                before.append(gen.get_state())
-                torch.randperm(fit_n, generator=gen, out=host.restarts[k])
+                before.append(g.get_state())
+                torch.randperm(fit_n, generator=g, out=hd.restarts[k])
+            return before
+
+        def upload(hd, before):
+            """The draws to the device from pinned memory."""
             if host.uploaded is not None:
                 host.uploaded.synchronize()     # the previous upload has left `pinned`
             total = fit_n + (1 + k_ahead) * cf
-            host.pinned[:fit_n].copy_(host.perm[:fit_n])
-            host.pinned[fit_n:fit_n + cf].copy_(host.init[:cf])
-            host.pinned[fit_n + cf:total].view(k_ahead, cf).copy_(host.restarts[:, :cf])
+            host.pinned[:fit_n].copy_(hd.perm[:fit_n])
+            host.pinned[fit_n:fit_n + cf].copy_(hd.init[:cf])
+            host.pinned[fit_n + cf:total].view(k_ahead, cf).copy_(hd.restarts[:, :cf])
             both = torch.empty(total, dtype=torch.int32, device=dev)
             both.copy_(host.pinned[:total], non_blocking=True)
             host.uploaded = torch.cuda.Event()
             host.uploaded.record()
             return both[:fit_n], both[fit_n:fit_n + cf], both[fit_n + cf:], before
+
+        cur = 0                                 # the draw set of the head being fitted
+
+        def draw():
+            return upload(host.sets[cur], draws(gen, host.sets[cur]))
 
         steps: dict = {}
 
@@ -308,9 +336,18 @@ class ProductPostingIndex:
             # the final steps are enqueued now, and again if an empty iteration past
             # those restarted on the GPU is redone below
             fit_assign = finalize(h)
-            # The next head's draws wait for this head's counts: they follow the restart
-            # draws this head takes, and drawing ahead for a guessed outcome costs host
-            # time the GPU then waits for
+            # The next head's draws follow the restart draws this head takes, which its
+            # counts decide.  While the host waits for them, a worker draws the next head's
+            # permutations into the other draw set for a guessed number of empty iterations
+            # (the last head's), from where the generator then stands: before the restart
+            # draw of that number, or after all k_ahead.  They are used if the guess holds
+            # and dropped otherwise, so the sequence of draws is the reference's either way.
+            ahead = None
+            if h + 1 < hkv and fit_trace is None and iters > 0 and k_ahead > 0:
+                guess = min(host.last_empties, k_ahead)
+                g_ahead = torch.Generator()
+                g_ahead.set_state(before_restart[guess] if guess < k_ahead else gen.get_state())
+                ahead = (guess, g_ahead, _draw_ahead_pool().submit(draws, g_ahead, host.sets[1 - cur]))
             if counted is not None:
                 counted.synchronize()
             empties = empty_iterations(0) if iters > 0 else []
@@ -319,8 +356,9 @@ class ProductPostingIndex:
             if fit_trace is not None:
                 # the sample rows each restarted iteration drew, for its empty clusters in
                 # ascending order (the GPU applied the first k_ahead of them)
-                drawn = {it: host.restarts[k][:int((counts_host[it] == 0).sum())].clone().long()
+                drawn = {it: host.sets[cur].restarts[k][:int((counts_host[it] == 0).sum())].clone().long()
                          for k, it in enumerate(empties[:k_ahead])}
+            host.last_empties = len(empties)
             # the GPU restarted the first k_ahead empty iterations; the next is restarted here
             it = empties[k_ahead] if len(empties) > k_ahead else -1
             while it >= 0:
@@ -359,6 +397,20 @@ class ProductPostingIndex:
                     partition=assign_all.to('cpu', copy=True).long()))
                 steps.clear()
             if h + 1 < hkv:
+                if ahead is not None:
+                    guess, g_ahead, fut = ahead
+                    before_next = fut.result()
+                    if len(empties) == guess:
+                        # the guess held (no restart drawn on the host either): the next
+                        # head's draws are the worker's, and the generator goes on from where
+                        # the worker's copy stopped
+                        gen.set_state(g_ahead.get_state())
+                        cur = 1 - cur
+                        sample_idx, init, restart_rows, before_restart = upload(host.sets[cur],
+                                                                                before_next)
+                        DRAW_AHEAD_STATS["used"] += 1
+                        continue
+                    DRAW_AHEAD_STATS["discarded"] += 1
                 sample_idx, init, restart_rows, before_restart = draw()
         width = int(totals.max().item())
         posting = posting_full[:, :width].contiguous()
