@@ -57,6 +57,7 @@ class _DrawBuffers:
                                   pin_memory=True)
         self.uploaded = None            # event after the last upload from `pinned`
         self.last_empties = 0           # empty k-means iterations of the last head fitted
+        self.head_empties: dict = {}    # and of each KV head in the last build of this shape
         self.counts = None              # pinned [iterations, C] cluster counts
 
     def counts_host(self, iters: int, c: int) -> torch.Tensor:
@@ -78,6 +79,7 @@ class _HeadDraws:
 
 _DRAW_BUFFERS: dict = {}
 _DRAW_AHEAD = None          # the worker thread that draws the next KV head's permutations ahead
+DRAW_AHEAD = True           # False: every head's draws on the host thread, after its counts
 DRAW_AHEAD_STATS = {"used": 0, "discarded": 0}
 
 
@@ -339,12 +341,16 @@ class ProductPostingIndex:
             # The next head's draws follow the restart draws this head takes, which its
             # counts decide.  While the host waits for them, a worker draws the next head's
             # permutations into the other draw set for a guessed number of empty iterations
-            # (the last head's), from where the generator then stands: before the restart
-            # draw of that number, or after all k_ahead.  They are used if the guess holds
-            # and dropped otherwise, so the sequence of draws is the reference's either way.
+            # of this head (its number in the last build of this shape, else the last
+            # head's), from where the generator then stands: before the restart draw of that
+            # number, or after all k_ahead.  They are used if the guess holds and dropped
+            # otherwise, so the sequence of draws is the reference's either way.
             ahead = None
-            if h + 1 < hkv and fit_trace is None and iters > 0 and k_ahead > 0:
-                guess = min(host.last_empties, k_ahead)
+            guess = host.head_empties.get(h, host.last_empties)
+            # past k_ahead empty iterations the host draws more restarts after the counts,
+            # which no draw made ahead can follow: then nothing is drawn ahead
+            if (DRAW_AHEAD and h + 1 < hkv and fit_trace is None and iters > 0 and k_ahead > 0
+                    and guess <= k_ahead):
                 g_ahead = torch.Generator()
                 g_ahead.set_state(before_restart[guess] if guess < k_ahead else gen.get_state())
                 ahead = (guess, g_ahead, _draw_ahead_pool().submit(draws, g_ahead, host.sets[1 - cur]))
@@ -358,7 +364,7 @@ class ProductPostingIndex:
                 # ascending order (the GPU applied the first k_ahead of them)
                 drawn = {it: host.sets[cur].restarts[k][:int((counts_host[it] == 0).sum())].clone().long()
                          for k, it in enumerate(empties[:k_ahead])}
-            host.last_empties = len(empties)
+            host.last_empties = host.head_empties[h] = len(empties)
             # the GPU restarted the first k_ahead empty iterations; the next is restarted here
             it = empties[k_ahead] if len(empties) > k_ahead else -1
             while it >= 0:
