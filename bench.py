@@ -415,18 +415,19 @@ def measure(args, config: int, steps: int, warmup: int, with_cpu: bool) -> dict:
     layer = SembloAttention(cfg, layer_name=f"bench.layer.{config}")
     result = {}
     if args.only in ("all", "prefill"):
+        # The prefill's host thread waits on the GPU inside the index build, so a
+        # full Python garbage collection there (about 20 ms over this process's
+        # objects) stalls the layer.  As a serving process does, the objects alive
+        # now are collected once and frozen out of later collections; collection
+        # itself stays on.  This is done before the warm-up: the step right after a
+        # collection runs about 2.5 ms slower, and the warm-up takes that step.
+        gc.collect()
+        gc.freeze()
         for i in range(warmup):
             run_prefill(layer, inp, conf)
             torch.cuda.synchronize()
             _log(f"warm-up {i} done")
         torch.cuda.synchronize()
-        # The prefill's host thread waits on the GPU inside the index build, so a
-        # full Python garbage collection there (about 20 ms over this process's
-        # objects) stalls the layer.  As a serving process does, the objects alive
-        # now are collected once and frozen out of later collections; collection
-        # itself stays on.
-        gc.collect()
-        gc.freeze()
         t0 = time.perf_counter()
         # events between the steps only log the spread, and events around every
         # attention launch time the kernel over the timed steps; nothing waits on them
