@@ -31,6 +31,24 @@ import torch
 PACK_ALIGN = 256        # rows: the packed store's width is a multiple of this
 
 
+def _upload(holder, table: torch.Tensor, dev) -> torch.Tensor:
+    """``table`` on the device by an asynchronous copy from pinned memory, so that
+    making or adopting an arena at the end of a prefill does not wait for the GPU to
+    finish it (a copy from pageable memory would).  The pinned copy stays on
+    ``holder`` until the next upload, which waits for this one first."""
+    if torch.device(dev).type != "cuda":
+        return table.to(dev, copy=True)
+    prev = getattr(holder, "_upload_done", None)
+    if prev is not None:
+        prev.synchronize()
+    pinned = table.pin_memory()
+    out = pinned.to(dev, non_blocking=True)
+    holder._upload_host = pinned
+    holder._upload_done = torch.cuda.Event()
+    holder._upload_done.record()
+    return out
+
+
 class DecodeArena:
     def __init__(self, index, *, reserve: int = 1024, suffix_block: int = 256,
                  suffix_splits: int = 8, shuffle_blocks: torch.Generator | None = None,
@@ -94,8 +112,8 @@ class DecodeArena:
             phys = phys[torch.randperm(self.suffix_blocks, generator=shuffle_blocks)]
         blocks = torch.arange(base, table.numel())
         table[base:] = phys[(blocks - base) % self.suffix_blocks]
-        self.suffix_table = table.to(dev)
-        self.prompt_length_t = torch.tensor([self.prompt_length], dtype=torch.int32, device=dev)
+        self.suffix_table = _upload(self, table, dev)
+        self.prompt_length_t = torch.full((1,), self.prompt_length, dtype=torch.int32, device=dev)
         self.steps = 0          # decode steps taken through the layer (host count, no device read)
 
     @property
@@ -164,7 +182,7 @@ class DecodeArena:
         table = torch.zeros(n, dtype=torch.int32)
         blocks = torch.arange(base, n)
         table[base:] = ((blocks - base) % self.suffix_blocks).to(torch.int32)
-        self.suffix_table.copy_(table)
+        self.suffix_table.copy_(_upload(self, table, self.suffix_table.device))
         self.prompt_length = int(prompt_length)
         self.first_prompt_length = int(prompt_length)
         self.prompt_length_t.fill_(int(prompt_length))
