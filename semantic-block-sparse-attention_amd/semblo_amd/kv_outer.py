@@ -121,7 +121,17 @@ class KVOuterPlan:
         cap, capped = partials_room(qn, hkv, c, hq // hkv, d, q.element_size(), guard)
         items, queue = build_work_list(self, hkv, c, qn, queries_per_item(hq // hkv), bucket_indptr,
                                        cap, capped, q.device)
-        self.work = (cap, capped, items, queue)
+        arrived = None
+        if capped:
+            # the overflow flag is final once the work list is built: copied to the host
+            # here, the chunk can be settled as soon as its plan is done, not after its
+            # attention
+            flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            flag.copy_(queue[QUEUE_OVERFLOW:QUEUE_OVERFLOW + 1], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            arrived = (ev, flag)
+        self.work = (cap, capped, items, queue, arrived)
 
     def tensors(self):
         """The device tensors a chunk's execution reads (for record_stream)."""
@@ -177,11 +187,16 @@ class PartialsGuard:
         self.reruns = 0
         self.cap_entries = 0
 
-    def watch(self, queue: torch.Tensor, rerun) -> None:
-        flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
-        flag.copy_(queue[QUEUE_OVERFLOW:QUEUE_OVERFLOW + 1], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
+    def watch(self, queue: torch.Tensor, rerun, arrived=None) -> None:
+        """``arrived``: (event, pinned flag) when the flag was copied already, on the
+        stream that built the work list; else it is copied here, behind the chunk."""
+        if arrived is None:
+            flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            flag.copy_(queue[QUEUE_OVERFLOW:QUEUE_OVERFLOW + 1], non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+        else:
+            ev, flag = arrived
         self._pending.append((self._next, ev, flag, rerun))
         self._next += 1
 
@@ -271,9 +286,10 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     local_o = torch.empty_like(q)
     local_lse = torch.empty(qn, hq, dtype=torch.float32, device=dev)
     s = _lib.stream(dev)
+    arrived = None
     if plan.work is not None and nnz is None and plan.work[:2] == (cap, capped):
         # built ahead on the plan's stream (KVOuterPlan.prepare_work); used once
-        items, queue = plan.work[2], plan.work[3]
+        items, queue, arrived = plan.work[2], plan.work[3], plan.work[4]
         plan.work = None
     else:
         items, queue = build_work_list(plan, hkv, c, qn, queries_per_item(g), bucket_indptr, cap, capped,
@@ -307,7 +323,7 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
                              sm_scale=sm_scale, local_kv=local_kv, chunk_start=chunk_start,
                              wstart=wstart, out=out, grid=grid, timing=timing)
         if guard is not None:
-            guard.watch(queue, rerun)
+            guard.watch(queue, rerun, arrived)
         elif int(queue[QUEUE_OVERFLOW].item()):
             rerun()
     stats = {"partials": nnz}

@@ -337,7 +337,9 @@ class SembloAttention:
 
         self.index = index
         # chunks whose partial rows were capped (kv_outer.partials_cap_bytes) are checked
-        # once, after the last chunk, and any that overflowed is run again
+        # once, after the last chunk is enqueued, and any that overflowed is run again;
+        # each flag comes from the chunk's plan (copied when its work list is built), so
+        # the check waits for the plans, not for the chunks' attention
         guard = PartialsGuard()
         for i in range(len(sparse)):
             enqueue_plan(i)
