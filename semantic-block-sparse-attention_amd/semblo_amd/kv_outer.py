@@ -333,6 +333,22 @@ def kv_outer_execute(q: torch.Tensor, packed_kv: torch.Tensor, plan: KVOuterPlan
     return out, stats
 
 
+_ZEROS: dict = {}
+
+
+def _zero_counts(n: int, dev) -> torch.Tensor:
+    """A zero int32 buffer of at least ``n`` entries on ``dev``, made once: the dense
+    chunks' work list reads it as empty cluster counts and never writes it."""
+    key = torch.device(dev)
+    z = _ZEROS.get(key)
+    if z is None or z.numel() < n:
+        z = torch.zeros(max(n, 1024), dtype=torch.int32, device=dev)
+        # once: the fill has landed before any stream reads the buffer
+        torch.cuda.current_stream(z.device).synchronize()
+        _ZEROS[key] = z
+    return z
+
+
 def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, sm_scale: float,
                            chunk_start: int = 0, out: torch.Tensor | None = None,
                            grid: int | None = None, timing=None) -> torch.Tensor:
@@ -346,7 +362,7 @@ def dense_causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     if k.shape[0] < chunk_start + qn:
         raise ValueError("k/v must cover every position up to the chunk's last query")
     qt = queries_per_item(g)
-    zero_counts = torch.zeros(hkv * 32, dtype=torch.int32, device=dev)
+    zero_counts = _zero_counts(hkv * 32, dev)
     bound = hkv * ((qn + qt - 1) // qt) + 1
     items = torch.empty(bound, ITEM_INTS, dtype=torch.int32, device=dev)
     queue = torch.empty(QUEUE_INTS, dtype=torch.int32, device=dev)
