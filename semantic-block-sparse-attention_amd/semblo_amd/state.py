@@ -83,12 +83,27 @@ DRAW_AHEAD = True           # False: every head's draws on the host thread, afte
 DRAW_AHEAD_STATS = {"used": 0, "discarded": 0}
 
 
-def _draw_ahead_pool():
-    global _DRAW_AHEAD
+_DRAW_AHEAD_LAST = None     # the last draw submitted to it
+
+
+def _draw_ahead_submit(fn, *args):
+    global _DRAW_AHEAD, _DRAW_AHEAD_LAST
     if _DRAW_AHEAD is None:
         from concurrent.futures import ThreadPoolExecutor
         _DRAW_AHEAD = ThreadPoolExecutor(max_workers=1, thread_name_prefix="sbsa-draws")
-    return _DRAW_AHEAD
+    _DRAW_AHEAD_LAST = _DRAW_AHEAD.submit(fn, *args)
+    return _DRAW_AHEAD_LAST
+
+
+def _draw_ahead_settle() -> None:
+    """Wait for a draw a build left running (one that raised before taking it): the
+    next build of the same shape draws into the same host buffers."""
+    fut = _DRAW_AHEAD_LAST
+    if fut is not None and not fut.done():
+        try:
+            fut.result()
+        except Exception:
+            pass
 
 
 def _draw_buffers(length: int, fit_n: int, c: int) -> _DrawBuffers:
@@ -230,6 +245,7 @@ class ProductPostingIndex:
         ws_bytes = _lib.query("sbsa_bucket_layout_workspace_bytes", length, c)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
 
+        _draw_ahead_settle()
         host = _draw_buffers(n_fit, fit_n, cf)
         counts_host = host.counts_host(n_it, cf)
 
@@ -353,7 +369,7 @@ class ProductPostingIndex:
                     and guess <= k_ahead):
                 g_ahead = torch.Generator()
                 g_ahead.set_state(before_restart[guess] if guess < k_ahead else gen.get_state())
-                ahead = (guess, g_ahead, _draw_ahead_pool().submit(draws, g_ahead, host.sets[1 - cur]))
+                ahead = (guess, g_ahead, _draw_ahead_submit(draws, g_ahead, host.sets[1 - cur]))
             if counted is not None:
                 counted.synchronize()
             empties = empty_iterations(0) if iters > 0 else []
